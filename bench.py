@@ -1,0 +1,255 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark: HBM GB/s and us/layer at 8K context over a 28-layer FP8-V
+paged cache (Qwen2.5-1.5B shape, B=1, S=1, 12q/2kv heads, D=128,
+T=8192, block size 16, blocks placed by a seeded permutation).
+
+One step = single-token decode attention over all 28 layers, inputs resident in HBM.
+  --mode multi : the 28 layers in one sdv_paged_attention call (3 launches per step)
+  --mode graph : 28 per-layer calls captured in one HIP graph (84 launches per step)
+The cache is written by the library's own quantize+append kernel from synthetic N(0,1)
+K/V.  Several cache replicas (default 4 x 178 MB) are rotated step by step so the 256 MB
+Infinity Cache cannot hold the working set.
+
+Prints ONE JSON line.  `value` is whole-step throughput in GB/s of algorithmic bytes
+(K + V + scales + Q + O + block table per layer).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "specdec-context-scaling_amd"))
+
+HBM_PEAK_GBS = 8000.0
+L, B, H, KV, D, T, S = 28, 1, 12, 2, 128, 8192, 1
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--mode", choices=("multi", "graph"), default="multi")
+    ap.add_argument("--replicas", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline leg")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph-leg", action="store_true", help="skip the per-layer HIP-graph figure")
+    return ap.parse_args()
+
+
+def phase_bytes():
+    """Algorithmic bytes per (sequence, layer) of each launch and of the whole call."""
+    from specdec_amd import workloads as wl
+
+    nblk = math.ceil(T / 16)
+    return {
+        "qk": T * KV * D * 2 + S * H * D * 2 + nblk * 4,
+        "pv": T * KV * D + T * KV * 4 + nblk * 4,
+        "reduce": S * H * D * 2,
+        "all": wl.bytes_attn(T, S, H, KV, D),
+    }
+
+
+def build_replicas(torch, dev, n):
+    from specdec_amd.engine.paged_cache import PagedKVCache
+    from specdec_amd.kernels import ops
+
+    reps = []
+    for r in range(n):
+        g = torch.Generator(device=dev)
+        g.manual_seed(1000 + r)
+        cache = PagedKVCache(KV, D, num_layers=L, batch=B, num_blocks=T // 16 + 64, device=dev, seed=2000 + r,
+                             growable=False)
+        cache.reserve(0, T)
+        slots = cache.slot_mapping([0], T)
+        k = torch.randn((L, T, KV, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((L, T, KV, D), generator=g, device=dev).to(torch.bfloat16)
+        ops.quant_append(v, slots, cache.k_pages, cache.v_pages, cache.v_scales, k)
+        cache.lengths[0] = T
+        del k, v
+        q = torch.randn((L, B, H, S, D), generator=g, device=dev).to(torch.bfloat16)
+        reps.append(dict(cache=cache, q=q, bt=cache.block_table(), sl=cache.seq_lens_tensor(),
+                         out=torch.empty_like(q)))
+    torch.cuda.synchronize()
+    return reps
+
+
+def time_steps(torch, step, steps, warmup, nrep):
+    for i in range(warmup):
+        step(i % nrep)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i % nrep)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from specdec_amd import _native
+    from specdec_amd.kernels import ops
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    reps = build_replicas(torch, dev, args.replicas)
+    ws_multi = ops.workspace(dev, ops.attention_workspace_bytes(L, B, H, KV, S, D, T))
+
+    def multi_step(r, phases=_native.PHASE_ALL):
+        rep = reps[r]
+        c = rep["cache"]
+        ops.paged_attention(rep["q"], c.k_pages, c.v_pages, c.v_scales, rep["bt"], rep["sl"], T,
+                            out=rep["out"], workspace_tensor=ws_multi, phases=phases)
+
+    def per_layer_calls(r):
+        rep = reps[r]
+        c = rep["cache"]
+        for layer in range(L):
+            kp, vp, vs = c.layer(layer)
+            ops.paged_attention(rep["q"][layer], kp, vp, vs, rep["bt"], rep["sl"], T, out=rep["out"][layer],
+                                workspace_tensor=ws_layer)
+
+    ws_layer = torch.empty(ops.attention_workspace_bytes(1, B, H, KV, S, D, T), dtype=torch.uint8, device=dev)
+    graphs = []
+    if args.mode == "graph" or not args.no_graph_leg:
+        for r in range(args.replicas):
+            per_layer_calls(r)  # warm the path outside capture
+        torch.cuda.synchronize()
+        for r in range(args.replicas):
+            gph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gph):
+                per_layer_calls(r)
+            graphs.append(gph)
+        torch.cuda.synchronize()
+
+    def graph_step(r):
+        graphs[r].replay()
+
+    pb = phase_bytes()
+    bytes_step = L * B * pb["all"]
+    main_step = multi_step if args.mode == "multi" else graph_step
+    ms = time_steps(torch, main_step, args.steps, args.warmup, args.replicas)
+    value = bytes_step / (ms * 1e-3) / 1e9
+
+    # Live per-launch timing of the multi-layer call: HIP events between the three launches
+    # (same stream, same workspace: together they are exactly one sdv_paged_attention call).
+    names = {"qk": _native.PHASE_QK, "pv": _native.PHASE_PV, "reduce": _native.PHASE_REDUCE}
+    evs = []
+    for i in range(args.warmup + args.steps):
+        r = i % args.replicas
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        marks[0].record()
+        for j, ph in enumerate(names.values()):
+            multi_step(r, ph)
+            marks[j + 1].record()
+        if i >= args.warmup:
+            evs.append(marks)
+    torch.cuda.synchronize()
+    per = {n: statistics.fmean(m[j].elapsed_time(m[j + 1]) for m in evs) * 1e3 for j, n in enumerate(names)}
+    dom = max(("qk", "pv"), key=lambda n: per[n])
+    achieved = L * B * pb[dom] / (per[dom] * 1e-6) / 1e9
+
+    graph_leg = None
+    if graphs:
+        gms = time_steps(torch, graph_step, args.steps, args.warmup, args.replicas)
+        graph_leg = {"us_per_step": round(gms * 1e3, 2), "us_per_layer": round(gms * 1e3 / L, 3),
+                     "GBps": round(bytes_step / (gms * 1e-3) / 1e9, 1),
+                     "frac_of_peak": round(bytes_step / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "launches_per_step": 3 * L}
+
+    traffic = None
+    tf = ROOT / "profiles" / "traffic_decode8k_multi.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get(dom)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": "decode-attn HBM GB/s (% of ~8 TB/s peak) + us/layer at 8K ctx, FP8-V cache",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_layer": round(ms * 1e3 / L, 3),
+        "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 K / fp8-e4m3 V, fp32 accumulate",
+        "data": "synthetic N(0,1) K/V (quantized by the library's append kernel), seeded",
+        "config": {"workload": "config 2: single-token decode attention, 28-layer Qwen2.5-1.5B-shaped "
+                               "FP8-V paged cache, T=8192",
+                   "batch": B, "q_heads": H, "kv_heads": KV, "head_dim": D, "seq_len": T, "layers": L,
+                   "block_size": 16, "launch": args.mode, "cache_replicas_rotated": args.replicas,
+                   "bytes_per_step": bytes_step, "parallelism": "none (1 GPU)"},
+        "per_launch_us": {k: round(v, 3) for k, v in per.items()},
+        "roofline": {"bound": "hbm", "kernel": f"{dom}_kernel (multi-layer call)", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "bytes_per_launch": L * B * pb[dom], "traffic": traffic},
+        "per_layer_graph": graph_leg,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(budget_s: float):
+    """The reference path restated in torch-CPU (oracle), one 8K layer per sample, timed here."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import attention as oatt
+    from specdec_amd import workloads as wl
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    g = wl.gen(7)
+    k = wl.randn_bf16((1, KV, T - 1, D), g)
+    v = wl.randn_bf16((1, KV, T - 1, D), g)
+    _, cache = oatt.vfp8_decode_step(None, wl.randn_bf16((1, H, 1, D), g), k, v)  # cache of T-1 tokens
+    q = wl.randn_bf16((1, H, 1, D), g)
+    kn = wl.randn_bf16((1, KV, 1, D), g)
+    vn = wl.randn_bf16((1, KV, 1, D), g)
+    oatt.vfp8_decode_step(cache, q, kn, vn)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        oatt.vfp8_decode_step(cache, q, kn, vn)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    per_layer_bytes = wl.bytes_attn(T, S, H, KV, D)
+    cpu_name = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(per_layer_bytes / med / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+            "us_per_layer": round(med * 1e6, 1),
+            "sample": f"{len(times)} single-layer 8K v_fp8 decode steps (quantize current V, cat K, dequantize + "
+                      f"cat V, kv_repeat, BF16 eager attention, append) in torch-CPU, median; a 28-layer step "
+                      f"is 28x this", "cpu": cpu_name, "torch": torch.__version__}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,149 @@
+/*
+ * sdv.h -- C ABI of the MI355X (gfx950) FP8-V paged decode hot path.
+ *
+ * Library: libsdv.so (built by hipcc from the .hip sources in specdec-context-scaling_amd/csrc).
+ * All tensor arguments are DEVICE pointers owned by the caller; the library allocates
+ * nothing per call.  Every entry point validates its arguments on the host, returns
+ * SDV_OK (0) or a negative status, launches asynchronously on `stream` (a hipStream_t,
+ * NULL = the legacy default stream) and is re-entrant (no mutable global state; calls
+ * that share a workspace buffer must be ordered on one stream).
+ *
+ * Paged cache layout (one layer; layers sit `*_layer_stride` elements apart):
+ *   k_pages  [num_blocks][kv_heads][16][head_dim]   bf16, token-major rows
+ *   v_pages  [num_blocks][kv_heads][head_dim][16]   E4M3FN codes, dimension-major in a page
+ *   v_scales [num_blocks][kv_heads][16]             fp32, one scale per (token, KV head)
+ * A token's slot is block * 16 + offset; block_table[b][j] is the physical block that
+ * holds tokens 16*j .. 16*j+15 of sequence b.
+ *
+ * Reference interfaces replaced (RichardF123/SpecDec-Context-Scaling):
+ *   sdv_quant_append     <- quantize_kv_fp8 (specdec/engine/model_self.py:304-314) applied
+ *                           to the current V (model_self.py:697-706) plus the v_fp8 cache
+ *                           append torch.cat of payload/scale (model_self.py:795-799) and the
+ *                           BF16 K write-back (model_self.py:721-722)
+ *   sdv_paged_attention  <- the v_fp8 read path (dequantize_kv_fp8 + cat, model_self.py:
+ *                           316-320, 715-728) and the eager GQA attention core
+ *                           (model_self.py:739-776); at op level it is what
+ *                           ops.attention(q, k, v, "cuda") (specdec/kernels/ops.py:67-76)
+ *                           -> pybind attention (specdec/kernels/cuda/bind.cpp:16)
+ *                           -> attention_cuda (specdec/kernels/cuda/attention.cu:244-288)
+ *                           computes, with FP8 V dequantized inside the kernel
+ *   sdv_attention_workspace_size  <- no counterpart (the reference allocates its score,
+ *                           softmax and kv_repeat temporaries inside torch)
+ *   sdv_fp8_encode       <- the tensor.to(torch.float8_e4m3fn) cast (model_self.py:312)
+ *   sdv_status_string    <- TORCH_CHECK messages (attention.cu:245-262)
+ */
+#ifndef SDV_H_
+#define SDV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SDV_BLOCK_SIZE 16
+#define SDV_ABI_VERSION 1
+
+enum sdv_status {
+    SDV_OK = 0,
+    SDV_ERR_NULL = -1,         /* a required pointer is NULL */
+    SDV_ERR_SHAPE = -2,        /* a size argument is out of range or inconsistent */
+    SDV_ERR_UNSUPPORTED = -3,  /* valid but not supported (head_dim, group size, scale mode) */
+    SDV_ERR_WORKSPACE = -4,    /* workspace NULL, too small or not 256-byte aligned */
+    SDV_ERR_ALIGN = -5,        /* a tensor pointer is not aligned as documented */
+    SDV_ERR_HIP = -6           /* the HIP runtime reported an error at launch */
+};
+
+/* scale_mode for sdv_quant_append: how s = max|v| / 448 is evaluated.
+ *  SDV_SCALE_DIV: IEEE fp32 division (torch on the CPU; the golden fixtures).
+ *  SDV_SCALE_RCP: max|v| * RN_f32(1/448) (torch's CUDA/ROCm kernels for a scalar divisor). */
+#define SDV_SCALE_DIV 0
+#define SDV_SCALE_RCP 1
+
+/*
+ * Kernel 1: fused V quantize (+ optional BF16 K copy) and paged append.
+ *
+ * v_new, k_new: bf16 [num_layers][n_tokens][kv_heads][head_dim] (layers in_layer_stride
+ *               elements apart; k_new may be NULL: K is then not written).
+ * slot_mapping: int32 [n_tokens]; a negative slot skips the token (padding).
+ * group_size must equal head_dim (the v_fp8 format: one scale per token and KV head).
+ * head_dim in {64, 128}.  Alignment: v_new/k_new/k_pages 4 B, v_pages 16 B, v_scales 4 B.
+ * Each (token, KV head) gets s = max|v| / 448 (s == 0 -> 1), payload RNE(v / s) in E4M3FN,
+ * bit-exact with the reference helper evaluated per scale_mode.
+ */
+int sdv_quant_append(const void* v_new, const void* k_new, const int32_t* slot_mapping,
+                     int32_t n_tokens, int32_t kv_heads, int32_t head_dim, int32_t group_size,
+                     int32_t num_layers, int64_t in_layer_stride,
+                     void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
+                     int64_t k_layer_stride, int64_t v_layer_stride, int64_t s_layer_stride,
+                     int32_t scale_mode, void* stream);
+
+/* Bytes of workspace sdv_paged_attention needs for these sizes (0 on invalid sizes). */
+size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q_heads,
+                                    int32_t kv_heads, int32_t q_len, int32_t head_dim,
+                                    int32_t max_seq_len);
+
+/*
+ * Kernels 2/3: paged GQA attention over BF16 K and FP8 V for q_len query rows per sequence
+ * (q_len = 1: decode; q_len = k+1 = 5: speculative verify; any q_len >= 1 is accepted).
+ *
+ * q, out: bf16, per layer [batch][q_heads][q_len][head_dim] (q_token_major = 0, the
+ *         reference op's (B,H,S,D)) or [batch][q_len][q_heads][head_dim] (q_token_major = 1,
+ *         the projection layout); layers are batch*q_heads*q_len*head_dim elements apart.
+ * seq_lens: int32 [batch] context length T_b including the q_len new tokens (1..max_seq_len;
+ *           the kernels clamp T_b to [0, max_seq_len], so no value can read out of bounds).
+ * block_table: int32 [batch][max_blocks_per_seq], max_blocks_per_seq >= ceil(max_seq_len/16);
+ *           an entry outside [0, num_blocks) is never dereferenced: its tokens are masked.
+ * Row i of the q_len-row block attends to keys j <= T_b - q_len + i (model_self.py:755-764).
+ * Numerics follow the eager path's rounding points: BF16 q.k, BF16 (q.k)/sqrt(D), fp32
+ * softmax normalised by the global max and sum, BF16 probabilities, BF16 dequantised V
+ * (fp32(code) * scale rounded once), fp32 accumulation, BF16 output.
+ * Alignment: q/out/k_pages/v_scales 16 B, v_pages 4 B, workspace 256 B.
+ */
+int sdv_paged_attention(const void* q, const void* k_pages, const void* v_pages,
+                        const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                        int64_t v_layer_stride, int64_t s_layer_stride,
+                        const int32_t* block_table, int32_t max_blocks_per_seq,
+                        const int32_t* seq_lens,
+                        int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                        int32_t q_len, int32_t head_dim, int32_t max_seq_len,
+                        int32_t q_token_major, void* workspace, size_t workspace_bytes,
+                        void* out, void* stream);
+
+/*
+ * Profiling split of sdv_paged_attention (same arguments plus phase_mask): runs only the
+ * selected launches -- SDV_PHASE_QK (scores + chunk statistics), SDV_PHASE_PV (global
+ * softmax, FP8-V dequant, partial p.V), SDV_PHASE_REDUCE (sum partials, BF16 out).  Calling
+ * it with SDV_PHASE_QK, then SDV_PHASE_PV, then SDV_PHASE_REDUCE on one stream with one
+ * workspace computes exactly what one sdv_paged_attention call computes; a timer can record
+ * events between the calls.  No counterpart in the reference.
+ */
+#define SDV_PHASE_QK 1
+#define SDV_PHASE_PV 2
+#define SDV_PHASE_REDUCE 4
+#define SDV_PHASE_ALL 7
+int sdv_paged_attention_phases(const void* q, const void* k_pages, const void* v_pages,
+                               const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                               int64_t v_layer_stride, int64_t s_layer_stride,
+                               const int32_t* block_table, int32_t max_blocks_per_seq,
+                               const int32_t* seq_lens,
+                               int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                               int32_t q_len, int32_t head_dim, int32_t max_seq_len,
+                               int32_t q_token_major, void* workspace, size_t workspace_bytes,
+                               void* out, void* stream, int32_t phase_mask);
+
+/* Elementwise fp32 -> E4M3FN (RNE, NaN beyond 464 / for Inf and NaN), device buffers. */
+int sdv_fp8_encode(const float* in, uint8_t* out, int64_t n, void* stream);
+
+/* Static, thread-safe description of a status code. */
+const char* sdv_status_string(int status);
+
+/* SDV_ABI_VERSION of the built library. */
+int sdv_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDV_H_ */

@@ -1,0 +1,104 @@
+// Device helpers for the gfx950 FP8-V decode kernels: BF16/E4M3FN conversions, DPP and
+// cross-row wave reductions, MFMA operand types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sdv {
+
+constexpr int kBlock = 16;   // tokens per page block
+constexpr int kWave = 64;    // CDNA wavefront width
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- BF16
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Round fp32 to the nearest BF16 (ties to even) and return it as fp32 (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
+
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  __bf16 h = (__bf16)x;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return bf16_bits(lo) | (bf16_bits(hi) << 16);
+}
+
+// ---------------------------------------------------------------- E4M3FN
+// Encode fp32 -> OCP E4M3FN code, round to nearest even; |x| > 464 (rounds past 448), Inf and
+// NaN give NaN (0x7F) with the input's sign.  Integer arithmetic on the fp32 bit pattern
+// for the normal range; the subnormal range (|x| < 2^-6) is rounded as RNE(|x| * 2^9), where
+// the power-of-two scaling is exact and v_rndne_f32 rounds ties to even.
+__device__ __forceinline__ uint32_t e4m3fn_encode(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  uint32_t r;
+  if (a > 0x43E80000u) {                 // > 464.0, Inf, NaN
+    r = 0x7Fu;
+  } else if (a >= 0x3C800000u) {         // >= 2^-6: normal E4M3
+    const uint32_t t = a + 0x7FFFFu + ((a >> 20) & 1u);
+    r = (t >> 20) - (120u << 3);         // fp32 exponent bias 127 -> E4M3 bias 7
+  } else {
+    r = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  }
+  return r | sign;
+}
+
+// E4M3FN code (low byte of `w` selected by `sel`) -> fp32, exact (v_cvt_f32_fp8, OCP on gfx950).
+__device__ __forceinline__ float e4m3fn_decode(uint32_t w, int sel) {
+  switch (sel) {
+    case 0: return __builtin_amdgcn_cvt_f32_fp8(w, 0);
+    case 1: return __builtin_amdgcn_cvt_f32_fp8(w, 1);
+    case 2: return __builtin_amdgcn_cvt_f32_fp8(w, 2);
+    default: return __builtin_amdgcn_cvt_f32_fp8(w, 3);
+  }
+}
+
+// ---------------------------------------------------------------- wave reductions
+// DPP row rotate (within each 16-lane row).
+template <int N>
+__device__ __forceinline__ float dpp_row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ uint32_t dpp_row_ror_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xF, 0xF, false);
+}
+
+// Max of a non-negative fp32 over all 64 lanes (unsigned compare of the bit patterns is
+// monotonic for non-negative floats and propagates NaN like torch.amax).  Wave-uniform result.
+__device__ __forceinline__ uint32_t wave_max_nonneg_bits(uint32_t v) {
+  v = max(v, dpp_row_ror_u<8>(v));
+  v = max(v, dpp_row_ror_u<4>(v));
+  v = max(v, dpp_row_ror_u<2>(v));
+  v = max(v, dpp_row_ror_u<1>(v));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0);
+  const uint32_t r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32);
+  const uint32_t r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// Exchange with the lane `mask` apart (mask in {16, 32}: across 16-lane rows).
+__device__ __forceinline__ float xor_lane(float v, int mask) {
+  const int src = (int)(threadIdx.x & 63) ^ mask;
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+
+// Online-softmax statistic merge: (m, l) with l = sum exp(s - m); m = -inf means empty.
+__device__ __forceinline__ void merge_stat(float& m, float& l, float m2, float l2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  const float a = (m == -INFINITY) ? 0.0f : l * expf(m - mn);
+  const float b = (m2 == -INFINITY) ? 0.0f : l2 * expf(m2 - mn);
+  m = mn;
+  l = a + b;
+}
+
+}  // namespace sdv

@@ -1,0 +1,70 @@
+"""Build and load the native library (mirror of specdec/kernels/build.py:17-52).
+
+The reference JIT-compiles its CUDA extension with ``torch.utils.cpp_extension.load``.
+Here the native code is a plain C-ABI shared library compiled ahead of time, in-tree, by
+``hipcc --offload-arch=gfx950`` (it cross-compiles without a GPU), and loaded with ctypes;
+``load()`` keeps the reference's name and its "build once, cache the module" behaviour.
+
+    python -m specdec_amd.build          # compile specdec_amd/libsdv.so
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+from . import _native
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR.parent / "csrc"
+INCLUDE = PKG_DIR.parent.parent / "include"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # Packed fp32 VALU ops stay off on this hardware pool (the host pass warns that it does
+    # not know the feature; that is expected).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise _native.SdvError("hipcc not found (ROCm is required to build libsdv.so)")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into specdec_amd/libsdv.so (always recompiles)."""
+    out = _native.LIB_PATH
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(tmp), *map(str, sources())]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    msgs = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise _native.SdvError(f"hipcc failed ({res.returncode}):\n{msgs}")
+    if verbose and msgs.strip():
+        print(msgs, file=sys.stderr)
+    os.replace(tmp, out)
+    return out
+
+
+def load():
+    """The loaded native library (ctypes.CDLL); raises SdvError if it has not been built."""
+    return _native.load()
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

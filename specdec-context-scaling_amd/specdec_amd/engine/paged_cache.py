@@ -1,0 +1,201 @@
+"""Paged FP8-V KV cache: page pool, block allocator and block tables.
+
+The reference keeps, per layer, ``{"fmt": "v_fp8", "k": BF16 (B,KV,T,D), "v": fp8 (B,KV,T,D),
+"v_scale": fp32 (B,KV,T,1)}`` and grows it with ``torch.cat`` every step
+(specdec/engine/model_self.py:778-800; docs/design_g4_cache_api.md:7-11).  This module
+stores the same bytes in pages of 16 tokens per KV head so an append writes only the new
+slots and attention reads pages in place:
+
+    k_pages  (L, num_blocks, KV, 16, D)  BF16
+    v_pages  (L, num_blocks, KV, D, 16)  E4M3FN codes (uint8), dimension-major per page
+    v_scales (L, num_blocks, KV, 16)     fp32
+
+All L layers share one block table per sequence (a token occupies the same slot in every
+layer).  The allocator hands out blocks from a free list; with ``seed`` the free list is a
+seeded permutation, which scatters a sequence's blocks the way a long-running server's
+fragmented pool does.  When the pool runs out it doubles (new page tensors, one copy).
+
+Ownership rule (the reference's trim returns views and its appends build new tensors, so an
+untrimmed handle keeps its data; here appends write pages in place): after
+``trim``/``set_length`` to n tokens, the next append overwrites slots n.. of that sequence,
+so any handle that still covers those positions sees the new tokens.  The SpecDec loop
+never reuses a pre-trim handle (specdec/engine/spec_dec.py:238,246).
+"""
+from __future__ import annotations
+
+import random
+
+import torch
+
+from ..kernels import ops
+
+BLOCK = ops.BLOCK
+
+
+class BlockAllocator:
+    """Free list of physical page blocks."""
+
+    def __init__(self, num_blocks: int, seed: int | None = None):
+        self.num_blocks = 0
+        self.seed = seed
+        self._rng = random.Random(seed) if seed is not None else None
+        self.free: list[int] = []
+        self.grow(num_blocks)
+
+    def grow(self, new_total: int) -> None:
+        fresh = list(range(self.num_blocks, new_total))
+        if self._rng is not None:
+            self._rng.shuffle(fresh)
+        # pop() takes from the end: keep ascending order for the unseeded allocator
+        self.free = fresh[::-1] + self.free
+        self.num_blocks = new_total
+
+    def alloc(self, n: int) -> list[int]:
+        if n > len(self.free):
+            raise RuntimeError(f"block pool exhausted: need {n}, {len(self.free)} free of {self.num_blocks}")
+        return [self.free.pop() for _ in range(n)]
+
+    def release(self, blocks) -> None:
+        self.free.extend(reversed(list(blocks)))
+
+
+class PagedKVCache:
+    """Page pool for ``num_layers`` layers and ``batch`` sequences."""
+
+    def __init__(self, kv_heads: int, head_dim: int, *, num_layers: int = 1, batch: int = 1,
+                 num_blocks: int | None = None, capacity_tokens: int = 256, device="cuda",
+                 seed: int | None = None, scale_mode: str = "div", growable: bool = True):
+        if head_dim not in (64, 128):
+            raise ValueError(f"head_dim must be 64 or 128 (got {head_dim})")
+        self.kv_heads, self.head_dim = kv_heads, head_dim
+        self.num_layers, self.batch = num_layers, batch
+        self.device = torch.device(device)
+        self.scale_mode = scale_mode
+        self.growable = growable
+        if num_blocks is None:
+            num_blocks = batch * -(-capacity_tokens // BLOCK)
+        self.alloc = BlockAllocator(num_blocks, seed)
+        self.k_pages, self.v_pages, self.v_scales = self._new_pages(num_blocks)
+        self.blocks: list[list[int]] = [[] for _ in range(batch)]
+        self.lengths: list[int] = [0] * batch
+        self._bt = None
+
+    # ------------------------------------------------------------------ storage
+    def _new_pages(self, nb: int):
+        L, KV, D = self.num_layers, self.kv_heads, self.head_dim
+        k = torch.zeros((L, nb, KV, BLOCK, D), dtype=torch.bfloat16, device=self.device)
+        v = torch.zeros((L, nb, KV, D, BLOCK), dtype=torch.uint8, device=self.device)
+        s = torch.ones((L, nb, KV, BLOCK), dtype=torch.float32, device=self.device)
+        return k, v, s
+
+    def _grow(self, min_blocks: int) -> None:
+        old = self.alloc.num_blocks
+        new = max(min_blocks, 2 * old)
+        k, v, s = self._new_pages(new)
+        k[:, :old].copy_(self.k_pages)
+        v[:, :old].copy_(self.v_pages)
+        s[:, :old].copy_(self.v_scales)
+        self.k_pages, self.v_pages, self.v_scales = k, v, s
+        self.alloc.grow(new)
+
+    def layer(self, i: int):
+        """(k_pages, v_pages, v_scales) of layer i (contiguous views)."""
+        return self.k_pages[i], self.v_pages[i], self.v_scales[i]
+
+    # ------------------------------------------------------------------ sequences
+    def reserve(self, seq: int, n_tokens: int) -> None:
+        """Make sure sequence `seq` has blocks for its first n_tokens positions."""
+        need = -(-n_tokens // BLOCK) - len(self.blocks[seq])
+        if need <= 0:
+            return
+        if need > len(self.alloc.free):
+            if not self.growable:
+                raise RuntimeError(f"block pool exhausted ({self.alloc.num_blocks} blocks) and growable=False")
+            self._grow(self.alloc.num_blocks + need)
+        self.blocks[seq].extend(self.alloc.alloc(need))
+        self._bt = None
+
+    def set_length(self, seq: int, n: int) -> None:
+        if n < 0 or n > len(self.blocks[seq]) * BLOCK:
+            raise ValueError(f"length {n} outside the reserved {len(self.blocks[seq]) * BLOCK} slots")
+        self.lengths[seq] = n
+
+    def free_sequence(self, seq: int) -> None:
+        self.alloc.release(self.blocks[seq])
+        self.blocks[seq] = []
+        self.lengths[seq] = 0
+        self._bt = None
+
+    def max_blocks(self) -> int:
+        return max(1, max(len(b) for b in self.blocks))
+
+    def block_table(self) -> torch.Tensor:
+        """int32 (batch, max_blocks) on the device; unused entries are -1 (never read)."""
+        if self._bt is None:
+            mb = self.max_blocks()
+            rows = [b + [-1] * (mb - len(b)) for b in self.blocks]
+            self._bt = torch.tensor(rows, dtype=torch.int32).to(self.device)
+        return self._bt
+
+    def slot_mapping(self, starts: list[int], count: int) -> torch.Tensor:
+        """int32 (batch * count,) slots of positions starts[b] .. starts[b]+count-1, token-major."""
+        out = []
+        for b in range(self.batch):
+            blks = self.blocks[b]
+            out.extend(blks[p // BLOCK] * BLOCK + p % BLOCK for p in range(starts[b], starts[b] + count))
+        return torch.tensor(out, dtype=torch.int32).to(self.device)
+
+    # ------------------------------------------------------------------ kernels
+    def append(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, starts: list[int] | None = None):
+        """Write S new tokens per sequence for one layer: k_new/v_new BF16 (B, S, KV, D).
+
+        Positions start at ``starts`` (default: the current lengths); lengths become
+        start + S.  Runs kernel 1 (quantize V, copy K) into the pages.
+        """
+        B, S = k_new.shape[0], k_new.shape[1]
+        starts = list(self.lengths) if starts is None else list(starts)
+        for b in range(B):
+            self.reserve(b, starts[b] + S)
+        slots = self.slot_mapping(starts, S)
+        kp, vp, vs = self.layer(layer)
+        ops.quant_append(v_new.reshape(B * S, self.kv_heads, self.head_dim), slots, kp, vp, vs,
+                         k_new.reshape(B * S, self.kv_heads, self.head_dim), scale_mode=self.scale_mode)
+        for b in range(B):
+            self.lengths[b] = starts[b] + S
+
+    def seq_lens_tensor(self, lengths: list[int] | None = None) -> torch.Tensor:
+        return torch.tensor(self.lengths if lengths is None else lengths, dtype=torch.int32).to(self.device)
+
+    def attend(self, layer: int, q: torch.Tensor, *, q_token_major: bool = False, lengths=None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+        """Attention of q (B,H,S,D) (or (B,S,H,D)) over this layer's pages at the current lengths."""
+        lengths = self.lengths if lengths is None else lengths
+        kp, vp, vs = self.layer(layer)
+        return ops.paged_attention(q, kp, vp, vs, self.block_table(), self.seq_lens_tensor(lengths),
+                                   max(lengths), q_token_major=q_token_major, out=out)
+
+    def gather(self, layer: int, seq: int, n: int | None = None):
+        """Contiguous (k BF16 (KV,T,D), v payload float8_e4m3fn (KV,T,D), v_scale fp32 (KV,T,1))."""
+        n = self.lengths[seq] if n is None else n
+        nb = -(-n // BLOCK)
+        idx = torch.tensor(self.blocks[seq][:nb], dtype=torch.long, device=self.device)
+        kp, vp, vs = self.layer(layer)
+        KV, D = self.kv_heads, self.head_dim
+        k = kp[idx].permute(1, 0, 2, 3).reshape(KV, nb * BLOCK, D)[:, :n]
+        v = vp[idx].permute(1, 0, 3, 2).reshape(KV, nb * BLOCK, D)[:, :n]
+        s = vs[idx].permute(1, 0, 2).reshape(KV, nb * BLOCK)[:, :n]
+        return k, v.contiguous().view(torch.float8_e4m3fn), s.unsqueeze(-1)
+
+    # ------------------------------------------------------------------ accounting
+    def logical_bytes_per_token_layer(self) -> int:
+        """K BF16 + V FP8 + fp32 scale per token per layer: 776 B for KV=2, D=128."""
+        return self.kv_heads * (2 * self.head_dim + self.head_dim + 4)
+
+    def footprint(self) -> dict:
+        tok = sum(self.lengths)
+        fp8 = tok * self.num_layers * self.logical_bytes_per_token_layer()
+        bf16 = tok * self.num_layers * self.kv_heads * 4 * self.head_dim
+        scales = tok * self.num_layers * self.kv_heads * 4
+        return {"tokens": tok, "fp8v_bytes": fp8, "bf16_bytes": bf16, "saved_frac": 1 - fp8 / max(bf16, 1),
+                "scale_frac_of_fp8v": scales / max(fp8, 1),
+                "pool_bytes": self.k_pages.numel() * 2 + self.v_pages.numel() + self.v_scales.numel() * 4}

@@ -1,0 +1,242 @@
+"""Torch-facing operators of the FP8-V path (mirror of specdec/kernels/ops.py).
+
+torch is plumbing here: tensors provide device memory and the current HIP stream; every
+computation runs in libsdv's gfx950 kernels through the C ABI (include/sdv.h).  Argument
+problems raise ``RuntimeError`` (:class:`specdec_amd.SdvError`), the way the reference
+op's TORCH_CHECKs do (specdec/kernels/cuda/attention.cu:245-262); an unknown backend raises
+``ValueError`` as in specdec/kernels/ops.py:76.
+
+Operators
+---------
+``quant_append``      kernel 1: V -> FP8 (per token and KV head max-abs/448 scale) plus the
+                      BF16 K copy, written into page slots.
+``paged_attention``   kernels 2/3: GQA decode / k+1-row verify over BF16 K + FP8 V pages.
+``attention``         the reference op's signature ``attention(q, k, v, backend)``
+                      (ops.py:67-76) over a contiguous v_fp8 cache: k BF16 (B,KV,T,D) and
+                      v given as the (payload, scale) pair the engine stores.
+``fp8_encode``        elementwise fp32 -> E4M3FN on the device.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _native
+from .._native import SdvError
+
+BLOCK = _native.BLOCK_SIZE
+_SCALE_MODES = {"div": _native.SCALE_DIV, "rcp": _native.SCALE_RCP}
+_BACKENDS = ("hip", "cuda")  # "cuda" is what reference call sites pass (patch.py:107)
+
+_WORKSPACES: dict = {}
+
+
+def _fail(msg: str):
+    raise SdvError(msg, _native.SDV_ERR_SHAPE)
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _need(t, name, dtypes, dev=None, ndim=None):
+    if not isinstance(t, torch.Tensor):
+        _fail(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        _fail(f"{name} must be on a HIP device (got {t.device})")
+    if dev is not None and t.device != dev:
+        _fail(f"{name} is on {t.device}, expected {dev}")
+    if t.dtype not in dtypes:
+        _fail(f"{name} must have dtype in {dtypes} (got {t.dtype})")
+    if not t.is_contiguous():
+        _fail(f"{name} must be contiguous")
+    if ndim is not None and t.dim() not in ndim:
+        _fail(f"{name} must have {ndim} dims (got {tuple(t.shape)})")
+
+
+def _pages_dims(k_pages, v_pages, v_scales, layered: bool):
+    lead = 1 if layered else 0
+    if k_pages.dim() != 4 + lead or v_pages.dim() != 4 + lead or v_scales.dim() != 3 + lead:
+        _fail(f"page tensors must be (..., num_blocks, KV, 16, D) / (..., num_blocks, KV, D, 16) / "
+              f"(..., num_blocks, KV, 16); got {tuple(k_pages.shape)}, {tuple(v_pages.shape)}, "
+              f"{tuple(v_scales.shape)}")
+    nb, kv, blk, d = k_pages.shape[lead:]
+    if blk != BLOCK or tuple(v_pages.shape[lead:]) != (nb, kv, d, BLOCK) or tuple(v_scales.shape[lead:]) != (nb, kv, BLOCK):
+        _fail(f"page shapes disagree: k {tuple(k_pages.shape)}, v {tuple(v_pages.shape)}, s {tuple(v_scales.shape)}")
+    if layered and not (k_pages.shape[0] == v_pages.shape[0] == v_scales.shape[0]):
+        _fail("page tensors disagree on the layer count")
+    return nb, kv, d
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A cached uint8 workspace of at least nbytes on (device, current stream)."""
+    dev = torch.device(device)
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def attention_workspace_bytes(num_layers: int, batch: int, q_heads: int, kv_heads: int, q_len: int,
+                              head_dim: int, max_seq_len: int) -> int:
+    n = _native.load().sdv_attention_workspace_size(num_layers, batch, q_heads, kv_heads, q_len,
+                                                    head_dim, max_seq_len)
+    if n == 0:
+        _fail(f"unsupported attention sizes L={num_layers} B={batch} H={q_heads} KV={kv_heads} "
+              f"S={q_len} D={head_dim} T={max_seq_len}")
+    return int(n)
+
+
+def quant_append(v_new: torch.Tensor, slot_mapping: torch.Tensor, k_pages: torch.Tensor,
+                 v_pages: torch.Tensor, v_scales: torch.Tensor, k_new: torch.Tensor | None = None,
+                 *, scale_mode: str = "div") -> None:
+    """Quantize V to FP8 and write V (and BF16 K when given) into page slots, in place.
+
+    v_new/k_new: BF16 (n_tokens, KV, D), or (L, n_tokens, KV, D) with layered pages.
+    slot_mapping: int32 (n_tokens,), slot = block * 16 + offset, negative = skip.
+    Pages: k (…, num_blocks, KV, 16, D) BF16; v (…, num_blocks, KV, D, 16) uint8 or
+    float8_e4m3fn; scales (…, num_blocks, KV, 16) fp32.
+    """
+    lib = _native.load()
+    _need(v_new, "v_new", (torch.bfloat16,), ndim=(3, 4))
+    dev = v_new.device
+    layered = v_new.dim() == 4
+    _need(k_pages, "k_pages", (torch.bfloat16,), dev)
+    _need(v_pages, "v_pages", (torch.uint8, torch.float8_e4m3fn), dev)
+    _need(v_scales, "v_scales", (torch.float32,), dev)
+    _need(slot_mapping, "slot_mapping", (torch.int32,), dev, ndim=(1,))
+    nb, kv, d = _pages_dims(k_pages, v_pages, v_scales, layered)
+    L = v_new.shape[0] if layered else 1
+    n_tokens = v_new.shape[-3]
+    if tuple(v_new.shape[-2:]) != (kv, d) or slot_mapping.shape[0] != n_tokens:
+        _fail(f"v_new {tuple(v_new.shape)} / slot_mapping {tuple(slot_mapping.shape)} do not match "
+              f"pages (KV={kv}, D={d})")
+    if layered and k_pages.shape[0] != L:
+        _fail(f"v_new has {L} layers, pages have {k_pages.shape[0]}")
+    if k_new is not None:
+        _need(k_new, "k_new", (torch.bfloat16,), dev)
+        if k_new.shape != v_new.shape:
+            _fail(f"k_new {tuple(k_new.shape)} != v_new {tuple(v_new.shape)}")
+    if scale_mode not in _SCALE_MODES:
+        raise ValueError(f"scale_mode must be one of {sorted(_SCALE_MODES)}")
+    per = lambda t: t[0].numel() if layered else 0  # noqa: E731  (elements per layer)
+    st = lib.sdv_quant_append(_p(v_new), _p(k_new), _p(slot_mapping), n_tokens, kv, d, d, L,
+                              per(v_new), _p(k_pages), _p(v_pages), _p(v_scales), nb,
+                              per(k_pages), per(v_pages), per(v_scales), _SCALE_MODES[scale_mode],
+                              _stream(dev))
+    _native.check(st, "sdv_quant_append")
+
+
+def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, v_scales: torch.Tensor,
+                    block_table: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int, *,
+                    q_token_major: bool = False, out: torch.Tensor | None = None,
+                    workspace_tensor: torch.Tensor | None = None,
+                    phases: int = _native.PHASE_ALL) -> torch.Tensor:
+    """GQA attention of q over paged BF16 K / FP8 V.
+
+    q: BF16 (B, H, S, D) (or (B, S, H, D) with q_token_major=True); a leading layer dimension
+    (L, ...) processes L layers in one launch with layered pages (L, num_blocks, ...).
+    block_table int32 (B, max_blocks); seq_lens int32 (B,) = context length including the S
+    new tokens, each <= max_seq_len.  Returns out shaped like q (BF16).
+    ``phases`` (profiling) runs a subset of the three launches; see sdv_paged_attention_phases.
+    """
+    lib = _native.load()
+    _need(q, "q", (torch.bfloat16,), ndim=(4, 5))
+    dev = q.device
+    layered = q.dim() == 5
+    _need(k_pages, "k_pages", (torch.bfloat16,), dev)
+    _need(v_pages, "v_pages", (torch.uint8, torch.float8_e4m3fn), dev)
+    _need(v_scales, "v_scales", (torch.float32,), dev)
+    _need(block_table, "block_table", (torch.int32,), dev, ndim=(2,))
+    _need(seq_lens, "seq_lens", (torch.int32,), dev, ndim=(1,))
+    nb, kv, d = _pages_dims(k_pages, v_pages, v_scales, layered)
+    L = q.shape[0] if layered else 1
+    if layered and k_pages.shape[0] != L:
+        _fail(f"q has {L} layers, pages have {k_pages.shape[0]}")
+    if q_token_major:
+        B, S, H, Dq = q.shape[-4:]
+    else:
+        B, H, S, Dq = q.shape[-4:]
+    if Dq != d or H % kv:
+        _fail(f"q {tuple(q.shape)} does not match pages (KV={kv}, D={d})")
+    if block_table.shape[0] != B or seq_lens.shape[0] != B:
+        _fail(f"block_table {tuple(block_table.shape)} / seq_lens {tuple(seq_lens.shape)} need batch {B}")
+    max_seq_len = int(max_seq_len)
+    if max_seq_len <= 0 or block_table.shape[1] * BLOCK < max_seq_len:
+        _fail(f"max_seq_len {max_seq_len} must be in [1, 16 * max_blocks = {block_table.shape[1] * BLOCK}]")
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _need(out, "out", (torch.bfloat16,), dev)
+        if out.shape != q.shape:
+            _fail(f"out {tuple(out.shape)} != q {tuple(q.shape)}")
+    nbytes = attention_workspace_bytes(L, B, H, kv, S, d, max_seq_len)
+    if workspace_tensor is None:
+        workspace_tensor = workspace(dev, nbytes)
+    per = lambda t: t[0].numel() if layered else 0  # noqa: E731
+    args = (_p(q), _p(k_pages), _p(v_pages), _p(v_scales), nb, per(k_pages), per(v_pages), per(v_scales),
+            _p(block_table), block_table.shape[1], _p(seq_lens), L, B, H, kv, S, d, max_seq_len,
+            int(bool(q_token_major)), _p(workspace_tensor), workspace_tensor.numel(), _p(out), _stream(dev))
+    if phases == _native.PHASE_ALL:
+        st = lib.sdv_paged_attention(*args)
+    else:
+        st = lib.sdv_paged_attention_phases(*args, int(phases))
+    _native.check(st, "sdv_paged_attention")
+    return out
+
+
+def pack_contiguous(k: torch.Tensor, v_payload: torch.Tensor, v_scale: torch.Tensor):
+    """Copy a contiguous v_fp8 cache (B,KV,T,D) into pages (one copy; block b*nbps + j is
+    tokens 16j.. of sequence b).  Returns (k_pages, v_pages, v_scales, block_table, seq_lens)."""
+    B, KV, T, D = k.shape
+    nbps = -(-T // BLOCK)
+    Tp = nbps * BLOCK
+    pad = Tp - T
+    kk = torch.nn.functional.pad(k, (0, 0, 0, pad)) if pad else k
+    vv = v_payload.view(torch.uint8)
+    vv = torch.nn.functional.pad(vv, (0, 0, 0, pad)) if pad else vv
+    ss = v_scale.reshape(B, KV, T)
+    ss = torch.nn.functional.pad(ss, (0, pad), value=1.0) if pad else ss
+    k_pages = kk.reshape(B, KV, nbps, BLOCK, D).permute(0, 2, 1, 3, 4).reshape(B * nbps, KV, BLOCK, D).contiguous()
+    v_pages = vv.reshape(B, KV, nbps, BLOCK, D).permute(0, 2, 1, 4, 3).reshape(B * nbps, KV, D, BLOCK).contiguous()
+    v_scales = ss.reshape(B, KV, nbps, BLOCK).permute(0, 2, 1, 3).reshape(B * nbps, KV, BLOCK).contiguous()
+    block_table = torch.arange(B * nbps, dtype=torch.int32, device=k.device).reshape(B, nbps)
+    seq_lens = torch.full((B,), T, dtype=torch.int32, device=k.device)
+    return k_pages, v_pages, v_scales, block_table, seq_lens
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v, backend: str = "hip") -> torch.Tensor:
+    """Reference op signature (specdec/kernels/ops.py:67-76) for the v_fp8 cache format.
+
+    q (B,H,S,D) BF16; k (B,KV,T,D) BF16; v = (payload float8_e4m3fn (B,KV,T,D),
+    scale fp32 (B,KV,T,1)) exactly as the reference cache stores it.  The FP8 payload is
+    dequantized inside the kernel; row i of the S-row block sees keys j <= T - S + i.
+    """
+    if backend not in _BACKENDS:
+        raise ValueError(backend)
+    if isinstance(v, torch.Tensor):
+        raise SdvError("the FP8-V backend needs v as (payload float8_e4m3fn, scale fp32); "
+                       "BF16 V is the reference's 'fp16' cache format, which this library does not serve",
+                       _native.SDV_ERR_UNSUPPORTED)
+    payload, scale = v
+    _need(q, "q", (torch.bfloat16,), ndim=(4,))
+    _need(k, "k", (torch.bfloat16,), q.device, ndim=(4,))
+    if payload.shape != k.shape or tuple(scale.shape) != tuple(k.shape[:3]) + (1,):
+        _fail(f"v payload {tuple(payload.shape)} / scale {tuple(scale.shape)} do not match k {tuple(k.shape)}")
+    kp, vp, vs, bt, sl = pack_contiguous(k.contiguous(), payload.contiguous(), scale.contiguous())
+    return paged_attention(q.contiguous(), kp, vp, vs, bt, sl, k.shape[2])
+
+
+def fp8_encode(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> uint8 E4M3FN codes (RNE; NaN beyond 464), computed on the device."""
+    _need(x, "x", (torch.float32,))
+    out = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    _native.check(_native.load().sdv_fp8_encode(_p(x), _p(out), x.numel(), _stream(x.device)), "sdv_fp8_encode")
+    return out

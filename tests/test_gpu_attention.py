@@ -1,0 +1,187 @@
+"""Kernels 2/3 (sdv_paged_attention) parity against the eager BF16 path.
+
+Reference: model_self.py:715-776 (dequantize the FP8 V cache, kv_repeat, BF16 q.k^T,
+/sqrt(D), offset-causal mask, fp32 softmax, BF16 probabilities, BF16 p.v).  Oracle:
+oracle.attention.eager_attention on the CPU.  Bar (BASELINE): max-abs <= 2e-2 and
+rel-L2 <= 1e-3 against the eager output, for every row of every case.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, announce
+from helpers import assert_close, bits16, build_pages, eager_ref, to_dev
+from oracle import attention as oatt
+from specdec_amd import workloads as wl
+from specdec_amd.engine.paged_cache import PagedKVCache
+from specdec_amd.kernels import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_case(dev, h, kv, d, lens, s, *, seed, fragmented=True, extra_blocks=7, q_token_major=False):
+    """Random q/k/v per sequence, oracle-built pages, one kernel call; returns (got, want)."""
+    g = wl.gen(seed)
+    B = len(lens)
+    nbs = [-(-t // 16) for t in lens]
+    nb = sum(nbs) + extra_blocks
+    order = torch.randperm(nb, generator=g).tolist() if fragmented else list(range(nb))
+    rows, at = [], 0
+    for n in nbs:
+        rows.append(order[at:at + n])
+        at += n
+    ks = [wl.randn_bf16((kv, t, d), g) for t in lens]
+    vs = [wl.randn_bf16((kv, t, d), g) for t in lens]
+    qs = [wl.randn_bf16((h, s, d), g) for _ in lens]
+    kp, vp, sp = build_pages(ks, vs, nb, rows)
+    mb = max(nbs)
+    bt = np.full((B, mb), -1, dtype=np.int32)
+    for b, r in enumerate(rows):
+        bt[b, :len(r)] = r
+    q = torch.stack(qs)                                   # (B, H, S, D)
+    qd = q.transpose(1, 2).contiguous() if q_token_major else q
+    out = ops.paged_attention(qd.to(dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(sp, dev),
+                              to_dev(bt, dev), to_dev(np.array(lens, dtype=np.int32), dev), max(lens),
+                              q_token_major=q_token_major)
+    torch.cuda.synchronize()
+    if q_token_major:
+        out = out.transpose(1, 2)
+    want = [eager_ref(qs[b][None], ks[b][None], vs[b][None], d)[0] for b in range(B)]
+    return out.cpu(), torch.stack(want)
+
+
+def test_config0_golden(cuda_device):
+    """One 1.5B layer, decode, T=2048, V written by kernel 1 (product path end to end)."""
+    announce("attn config0 golden")
+    q, k, v = wl.config0(seed=0)
+    cache = PagedKVCache(2, 128, capacity_tokens=2048, device=cuda_device)
+    kt = k[0].transpose(0, 1).unsqueeze(0).contiguous()   # (1, T, KV, D)
+    vt = v[0].transpose(0, 1).unsqueeze(0).contiguous()
+    cache.append(0, kt.to(cuda_device), vt.to(cuda_device))
+    out = cache.attend(0, q.to(cuda_device)).cpu()
+    z = np.load(GOLDEN / "attn_eager.npz")
+    want = torch.from_numpy(z["cfg0_out"].view(np.int16)).view(torch.bfloat16)
+    stats = assert_close(out, want, "cfg0 vs golden")
+    print("cfg0", stats)
+    assert_close(out, eager_ref(q, k, v, 128), "cfg0 vs oracle on this host")
+
+
+@pytest.mark.parametrize("t", [2048, 8192])
+def test_decode_target_shape(cuda_device, t):
+    announce(f"attn decode 12/2/128 T={t}")
+    got, want = _run_case(cuda_device, 12, 2, 128, [t], 1, seed=40 + t)
+    print("decode", t, assert_close(got, want, f"decode T={t}"))
+
+
+@pytest.mark.parametrize("t", [2048, 4096, 8192])
+def test_verify_five_rows(cuda_device, t):
+    announce(f"attn verify S=5 T={t}")
+    got, want = _run_case(cuda_device, 12, 2, 128, [t], 5, seed=50 + t)
+    for i in range(5):
+        assert_close(got[:, :, i], want[:, :, i], f"verify T={t} row {i}")
+
+
+@pytest.mark.parametrize("t", [2048, 8192])
+def test_draft_shape_d64(cuda_device, t):
+    announce(f"attn draft 14/2/64 T={t}")
+    got, want = _run_case(cuda_device, 14, 2, 64, [t], 1, seed=60 + t)
+    print("draft", t, assert_close(got, want, f"draft T={t}"))
+
+
+def test_small_and_ragged_edges(cuda_device):
+    """T=1, T<16, T not a multiple of 16 or 32, odd block counts, S>T-1 edges."""
+    announce("attn ragged small edges")
+    lens = [1, 5, 16, 17, 31, 33, 48, 100, 1000]
+    got, want = _run_case(cuda_device, 12, 2, 128, lens, 1, seed=70)
+    for b, t in enumerate(lens):
+        assert_close(got[b], want[b], f"T={t}")
+    lens = [5, 6, 21, 64, 129]
+    got, want = _run_case(cuda_device, 12, 2, 128, lens, 5, seed=71)
+    for b, t in enumerate(lens):
+        assert_close(got[b], want[b], f"S=5 T={t}")
+
+
+def test_token_major_q_layout(cuda_device):
+    announce("attn token-major q")
+    got, want = _run_case(cuda_device, 12, 2, 128, [300, 777], 5, seed=72, q_token_major=True)
+    assert_close(got, want, "token-major")
+
+
+def test_config4_batch32_ragged(cuda_device):
+    """B=32, T_b ~ U{2048..32768}, fragmented pool: every sequence within the bar."""
+    announce("attn config4 B=32 ragged")
+    lens = wl.ragged_lengths(32, 2048, 32768, seed=4)
+    got, want = _run_case(cuda_device, 12, 2, 128, lens, 1, seed=73)
+    worst = 0.0
+    for b, t in enumerate(lens):
+        worst = max(worst, assert_close(got[b], want[b], f"b={b} T={t}")["rel_l2"])
+    print("config4 worst rel_l2", worst)
+
+
+def test_deterministic_bitwise(cuda_device):
+    announce("attn determinism")
+    g = wl.gen(80)
+    t = 5000
+    kp, vp, sp = build_pages([wl.randn_bf16((2, t, 128), g)], [wl.randn_bf16((2, t, 128), g)], 320,
+                             [list(range(313))])
+    bt = to_dev(np.arange(313, dtype=np.int32)[None], cuda_device)
+    args = (to_dev(kp, cuda_device), to_dev(vp, cuda_device), to_dev(sp, cuda_device), bt,
+            torch.tensor([t], dtype=torch.int32, device=cuda_device), t)
+    q = wl.randn_bf16((1, 12, 5, 128), g).to(cuda_device)
+    o1 = ops.paged_attention(q, *args).clone()
+    o2 = ops.paged_attention(q, *args)
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+def test_invalid_block_ids_are_masked(cuda_device):
+    """Block-table entries outside [0, num_blocks) are never read; their tokens drop out."""
+    announce("attn invalid block ids")
+    g = wl.gen(81)
+    t, d = 64, 128
+    k = wl.randn_bf16((2, t, d), g)
+    v = wl.randn_bf16((2, t, d), g)
+    kp, vp, sp = build_pages([k], [v], 4, [[0, 1, 2, 3]])
+    q = wl.randn_bf16((1, 12, 1, d), g)
+    bt = np.array([[0, 1000, 2, -5]], dtype=np.int32)      # blocks 1 and 3 invalid
+    out = ops.paged_attention(q.to(cuda_device), to_dev(kp, cuda_device), to_dev(vp, cuda_device),
+                              to_dev(sp, cuda_device), to_dev(bt, cuda_device),
+                              torch.tensor([t], dtype=torch.int32, device=cuda_device), t).cpu()
+    keep = torch.cat([torch.arange(0, 16), torch.arange(32, 48)])
+    want = eager_ref(q, k[None][:, :, keep], v[None][:, :, keep], d)
+    assert_close(out, want, "masked blocks")
+
+
+def test_reference_op_signature(cuda_device):
+    """ops.attention(q, k, (payload, scale)) over a contiguous v_fp8 cache (the engine's dicts)."""
+    announce("ops.attention contiguous v_fp8")
+    g = wl.gen(82)
+    q = wl.randn_bf16((1, 12, 5, 128), g)
+    k = wl.randn_bf16((1, 2, 333, 128), g)
+    v = wl.randn_bf16((1, 2, 333, 128), g)
+    from oracle import quant as oq
+    pq, ps = oq.quantize_kv_fp8(v, 128)
+    out = ops.attention(q.to(cuda_device), k.to(cuda_device), (pq.to(cuda_device), ps.to(cuda_device)),
+                        backend="hip").cpu()
+    assert_close(out, eager_ref(q, k, v, 128), "ops.attention")
+    with pytest.raises(ValueError):
+        ops.attention(q.to(cuda_device), k.to(cuda_device), (pq, ps), backend="triton")
+
+
+def test_multi_layer_launch_matches_per_layer(cuda_device):
+    """L layers in one launch == L single-layer launches, bit for bit."""
+    announce("attn multi-layer launch")
+    L, t = 4, 3000
+    cache = PagedKVCache(2, 128, num_layers=L, capacity_tokens=t, device=cuda_device, seed=3)
+    g = wl.gen(83)
+    for layer in range(L):
+        cache.append(layer, wl.randn_bf16((1, t, 2, 128), g).to(cuda_device),
+                     wl.randn_bf16((1, t, 2, 128), g).to(cuda_device), starts=[0])
+    q = wl.randn_bf16((L, 1, 12, 1, 128), g).to(cuda_device)
+    multi = ops.paged_attention(q, cache.k_pages, cache.v_pages, cache.v_scales, cache.block_table(),
+                                cache.seq_lens_tensor(), t)
+    for layer in range(L):
+        single = cache.attend(layer, q[layer])
+        # same chunk plan here (the plan depends on L only through the total block count)
+        assert torch.equal(single.view(torch.int16), multi[layer].view(torch.int16)), layer

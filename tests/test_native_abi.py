@@ -1,0 +1,106 @@
+"""libsdv.so loads on a machine without a GPU, exports every symbol include/sdv.h declares,
+and rejects bad arguments on the host before any HIP call (no compute calls here)."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+from specdec_amd import _native, build
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        build.build()
+    return _native.load()
+
+
+def _declared():
+    text = (ROOT / "include" / "sdv.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(sdv_\w+)\s*\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert names == sorted(_native.SIGNATURES), names
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.sdv_abi_version() == _native.ABI_VERSION
+    for st in range(0, -7, -1):
+        assert _native.status_string(st) not in ("", "unknown status"), st
+    assert _native.status_string(-99) == "unknown status"
+
+
+P = ctypes.c_void_p(0x1000)   # fake, 256-aligned non-null device pointers: never dereferenced
+N = None
+
+
+def _attn(lib, **kw):
+    a = dict(q=P, k=P, v=P, s=P, nb=8, kls=0, vls=0, sls=0, bt=P, mb=4, sl=P, L=1, B=1, H=12, KV=2, S=1,
+             D=128, T=64, tm=0, ws=P, wsb=1 << 30, out=P, st=N)
+    a.update(kw)
+    return lib.sdv_paged_attention(a["q"], a["k"], a["v"], a["s"], a["nb"], a["kls"], a["vls"], a["sls"],
+                                   a["bt"], a["mb"], a["sl"], a["L"], a["B"], a["H"], a["KV"], a["S"], a["D"],
+                                   a["T"], a["tm"], a["ws"], a["wsb"], a["out"], a["st"])
+
+
+def test_attention_host_validation(lib):
+    assert _attn(lib, q=N) == _native.SDV_ERR_NULL
+    assert _attn(lib, D=96) == _native.SDV_ERR_UNSUPPORTED
+    assert _attn(lib, H=13) == _native.SDV_ERR_SHAPE            # H % KV != 0
+    assert _attn(lib, T=0) == _native.SDV_ERR_SHAPE
+    assert _attn(lib, mb=3) == _native.SDV_ERR_SHAPE            # 3 blocks < 64 tokens
+    assert _attn(lib, tm=2) == _native.SDV_ERR_SHAPE
+    assert _attn(lib, L=2, kls=10) == _native.SDV_ERR_SHAPE     # layer stride smaller than a layer
+    assert _attn(lib, ws=N) == _native.SDV_ERR_WORKSPACE
+    assert _attn(lib, wsb=16) == _native.SDV_ERR_WORKSPACE
+    assert _attn(lib, ws=ctypes.c_void_p(0x1010)) == _native.SDV_ERR_WORKSPACE   # not 256-aligned
+    assert _attn(lib, q=ctypes.c_void_p(0x1002)) == _native.SDV_ERR_ALIGN
+
+
+def _quant(lib, **kw):
+    a = dict(v=P, k=N, sl=P, n=16, KV=2, D=128, gs=128, L=1, ils=0, kp=P, vp=P, vs=P, nb=8, kls=0, vls=0,
+             sls=0, mode=0, st=N)
+    a.update(kw)
+    return lib.sdv_quant_append(a["v"], a["k"], a["sl"], a["n"], a["KV"], a["D"], a["gs"], a["L"], a["ils"],
+                                a["kp"], a["vp"], a["vs"], a["nb"], a["kls"], a["vls"], a["sls"], a["mode"],
+                                a["st"])
+
+
+def test_quant_host_validation(lib):
+    assert _quant(lib, v=N) == _native.SDV_ERR_NULL
+    assert _quant(lib, k=P, kp=N) == _native.SDV_ERR_NULL
+    assert _quant(lib, gs=32) == _native.SDV_ERR_UNSUPPORTED    # GROUP_SIZE ablation is not v_fp8
+    assert _quant(lib, D=256, gs=256) == _native.SDV_ERR_UNSUPPORTED
+    assert _quant(lib, mode=7) == _native.SDV_ERR_UNSUPPORTED
+    assert _quant(lib, n=-1) == _native.SDV_ERR_SHAPE
+    assert _quant(lib, L=2, ils=5) == _native.SDV_ERR_SHAPE
+    assert _quant(lib, vp=ctypes.c_void_p(0x1004)) == _native.SDV_ERR_ALIGN
+    assert _quant(lib, n=0) == _native.SDV_OK                  # nothing to do, no launch
+
+
+def test_workspace_size_is_pure_host(lib):
+    a = lib.sdv_attention_workspace_size(1, 1, 12, 2, 1, 128, 8192)
+    b = lib.sdv_attention_workspace_size(28, 1, 12, 2, 1, 128, 8192)
+    c = lib.sdv_attention_workspace_size(1, 1, 12, 2, 5, 128, 8192)
+    assert 0 < a < b and a < c
+    assert a % 256 == 0
+    assert lib.sdv_attention_workspace_size(1, 1, 12, 2, 1, 96, 8192) == 0
+    assert lib.sdv_attention_workspace_size(1, 1, 12, 5, 1, 128, 8192) == 0
+
+
+def test_encode_validation(lib):
+    assert lib.sdv_fp8_encode(N, P, 4, N) == _native.SDV_ERR_NULL
+    assert lib.sdv_fp8_encode(P, P, -1, N) == _native.SDV_ERR_SHAPE
+    assert lib.sdv_fp8_encode(P, P, 0, N) == _native.SDV_OK
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_native.SdvError, match="not built"):
+        _native.load(tmp_path / "libsdv.so")

@@ -58,7 +58,7 @@ def phase_bytes():
     }
 
 
-def build_replicas(torch, dev, n):
+def build_replicas(torch, dev, n, scattered=True):
     from specdec_amd.engine.paged_cache import PagedKVCache
     from specdec_amd.kernels import ops
 
@@ -66,8 +66,8 @@ def build_replicas(torch, dev, n):
     for r in range(n):
         g = torch.Generator(device=dev)
         g.manual_seed(1000 + r)
-        cache = PagedKVCache(KV, D, num_layers=L, batch=B, num_blocks=T // 16 + 64, device=dev, seed=2000 + r,
-                             growable=False)
+        cache = PagedKVCache(KV, D, num_layers=L, batch=B, num_blocks=T // 16 + 64, device=dev,
+                             seed=(2000 + r) if scattered else None, growable=False)
         cache.reserve(0, T)
         slots = cache.slot_mapping([0], T)
         k = torch.randn((L, T, KV, D), generator=g, device=dev).to(torch.bfloat16)
@@ -147,21 +147,15 @@ def main():
     ms = time_steps(torch, main_step, args.steps, args.warmup, args.replicas)
     value = bytes_step / (ms * 1e-3) / 1e9
 
-    # Live per-launch timing of the multi-layer call: HIP events between the three launches
-    # (same stream, same workspace: together they are exactly one sdv_paged_attention call).
+    # Live per-launch timing of the multi-layer call: each of the three launches timed on its
+    # own, back to back on the library's stream with HIP events (torch's current stream is the
+    # stream the library launches on).  The launches after the first reuse the workspace of
+    # the preceding full calls, so they read valid scores and statistics.
     names = {"qk": _native.PHASE_QK, "pv": _native.PHASE_PV, "reduce": _native.PHASE_REDUCE}
-    evs = []
-    for i in range(args.warmup + args.steps):
-        r = i % args.replicas
-        marks = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        marks[0].record()
-        for j, ph in enumerate(names.values()):
-            multi_step(r, ph)
-            marks[j + 1].record()
-        if i >= args.warmup:
-            evs.append(marks)
-    torch.cuda.synchronize()
-    per = {n: statistics.fmean(m[j].elapsed_time(m[j + 1]) for m in evs) * 1e3 for j, n in enumerate(names)}
+    per = {}
+    for name, ph in names.items():
+        per[name] = time_steps(torch, lambda r, ph=ph: multi_step(r, ph), args.steps, args.warmup,
+                               args.replicas) * 1e3
     dom = max(("qk", "pv"), key=lambda n: per[n])
     achieved = L * B * pb[dom] / (per[dom] * 1e-6) / 1e9
 

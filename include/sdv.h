@@ -9,7 +9,9 @@
  * that share a workspace buffer must be ordered on one stream).
  *
  * Paged cache layout (one layer; layers sit `*_layer_stride` elements apart):
- *   k_pages  [num_blocks][kv_heads][16][head_dim]   bf16, token-major rows
+ *   k_pages  [num_blocks][kv_heads][head_dim/8][16][8]  bf16: token t, dim d of a page sits at
+ *                                                   ((d/8)*16 + t)*8 + d%8 (8-dim chunks, so
+ *                                                   one 1 KiB load feeds a 16x32 MFMA tile)
  *   v_pages  [num_blocks][kv_heads][head_dim][16]   E4M3FN codes, dimension-major in a page
  *   v_scales [num_blocks][kv_heads][16]             fp32, one scale per (token, KV head)
  * A token's slot is block * 16 + offset; block_table[b][j] is the physical block that

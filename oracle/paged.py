@@ -5,7 +5,8 @@ fp8, "v_scale": (B,KV,T,1) fp32}`` grown by ``torch.cat`` (model_self.py:778-800
 docs/design_g4_cache_api.md:7-11).  This build stores the same bytes in pages of
 ``BLOCK = 16`` tokens per KV head, addressed through a block table:
 
-* ``k_pages [num_blocks, KV, 16, D]``  uint16 (BF16 bits), token-major rows;
+* ``k_pages [num_blocks, KV, D/8, 16, 8]`` uint16 (BF16 bits): 8-dimension chunks, then
+  tokens, then the 8 dimensions of the chunk;
 * ``v_pages [num_blocks, KV, D, 16]``  uint8 (E4M3FN codes), dimension-major inside a page;
 * ``v_scales[num_blocks, KV, 16]``     float32;
 * a token's slot is ``block * 16 + offset``.
@@ -22,7 +23,7 @@ BLOCK = 16
 
 
 def alloc(num_blocks: int, kv_heads: int, head_dim: int):
-    k_pages = np.zeros((num_blocks, kv_heads, BLOCK, head_dim), dtype=np.uint16)
+    k_pages = np.zeros((num_blocks, kv_heads, head_dim // 8, BLOCK, 8), dtype=np.uint16)
     v_pages = np.zeros((num_blocks, kv_heads, head_dim, BLOCK), dtype=np.uint8)
     v_scales = np.zeros((num_blocks, kv_heads, BLOCK), dtype=np.float32)
     return k_pages, v_pages, v_scales
@@ -35,7 +36,8 @@ def write(k_pages, v_pages, v_scales, k_bits, v_payload, v_scale, slot_mapping) 
     blk = slots[ok] // BLOCK
     off = slots[ok] % BLOCK
     if k_bits is not None:
-        k_pages[blk, :, off, :] = np.asarray(k_bits)[ok]
+        kb = np.asarray(k_bits)[ok]                         # (n, KV, D)
+        k_pages[blk, :, :, off, :] = kb.reshape(kb.shape[0], kb.shape[1], -1, 8)
     v_pages[blk, :, :, off] = np.asarray(v_payload)[ok]
     v_scales[blk, :, off] = np.asarray(v_scale)[ok]
 
@@ -44,8 +46,8 @@ def gather(k_pages, v_pages, v_scales, block_row, seq_len: int):
     """-> k (KV,T,D) uint16, v (KV,T,D) uint8, s (KV,T) f32 for one sequence of length seq_len."""
     nb = -(-seq_len // BLOCK)
     blocks = np.asarray(block_row[:nb], dtype=np.int64)
-    kv, d = k_pages.shape[1], k_pages.shape[3]
-    k = k_pages[blocks].transpose(1, 0, 2, 3).reshape(kv, nb * BLOCK, d)[:, :seq_len]
+    kv, d = k_pages.shape[1], k_pages.shape[2] * 8
+    k = k_pages[blocks].transpose(1, 0, 3, 2, 4).reshape(kv, nb * BLOCK, d)[:, :seq_len]
     v = v_pages[blocks].transpose(1, 0, 3, 2).reshape(kv, nb * BLOCK, d)[:, :seq_len]
     s = v_scales[blocks].transpose(1, 0, 2).reshape(kv, nb * BLOCK)[:, :seq_len]
     return k, v, s

@@ -5,6 +5,8 @@
 // payload = RNE_E4M3FN(v / s), and the append of payload, scale and BF16 K
 // (model_self.py:721-722, 795-799) -- written into pages instead of concatenated.
 //
+// K is copied into the page's [D/8][16][8] chunk layout (see include/sdv.h).
+//
 // One wavefront handles 16 consecutive tokens of one KV head of one layer.  Lane l owns
 // head_dim/64 adjacent dimensions, so each token's 128-dim row is one coalesced 256-byte
 // load and the max-abs is a wave reduction (DPP row rotations + cross-row readlanes).
@@ -91,8 +93,10 @@ __global__ __launch_bounds__(64) void quant_append_kernel(QuantArgs a) {
     const int blk = slot >> 4, off = slot & (kBlock - 1);
     const int64_t page = (int64_t)blk * KV + kvh;
     if (kin) {
+      // K page: [D/8 chunks][16 tokens][8 dims]; lane's dims DPL*lane.. sit in chunk DPL*lane/8
       const uint16_t* ksrc = kin + ((int64_t)(t0 + i) * KV + kvh) * D + DPL * lane;
-      uint16_t* kdst = kp + (page * kBlock + off) * D + DPL * lane;
+      const int d0 = DPL * lane;
+      uint16_t* kdst = kp + page * kBlock * D + ((d0 >> 3) * kBlock + off) * 8 + (d0 & 7);
       if (DPL == 2)
         *reinterpret_cast<uint32_t*>(kdst) = *reinterpret_cast<const uint32_t*>(ksrc);
       else

@@ -6,7 +6,7 @@ The reference keeps, per layer, ``{"fmt": "v_fp8", "k": BF16 (B,KV,T,D), "v": fp
 stores the same bytes in pages of 16 tokens per KV head so an append writes only the new
 slots and attention reads pages in place:
 
-    k_pages  (L, num_blocks, KV, 16, D)  BF16
+    k_pages  (L, num_blocks, KV, D/8, 16, 8)  BF16 (8-dimension chunks x tokens x 8)
     v_pages  (L, num_blocks, KV, D, 16)  E4M3FN codes (uint8), dimension-major per page
     v_scales (L, num_blocks, KV, 16)     fp32
 
@@ -83,7 +83,7 @@ class PagedKVCache:
     # ------------------------------------------------------------------ storage
     def _new_pages(self, nb: int):
         L, KV, D = self.num_layers, self.kv_heads, self.head_dim
-        k = torch.zeros((L, nb, KV, BLOCK, D), dtype=torch.bfloat16, device=self.device)
+        k = torch.zeros((L, nb, KV, D // 8, BLOCK, 8), dtype=torch.bfloat16, device=self.device)
         v = torch.zeros((L, nb, KV, D, BLOCK), dtype=torch.uint8, device=self.device)
         s = torch.ones((L, nb, KV, BLOCK), dtype=torch.float32, device=self.device)
         return k, v, s
@@ -181,7 +181,7 @@ class PagedKVCache:
         idx = torch.tensor(self.blocks[seq][:nb], dtype=torch.long, device=self.device)
         kp, vp, vs = self.layer(layer)
         KV, D = self.kv_heads, self.head_dim
-        k = kp[idx].permute(1, 0, 2, 3).reshape(KV, nb * BLOCK, D)[:, :n]
+        k = kp[idx].permute(1, 0, 3, 2, 4).reshape(KV, nb * BLOCK, D)[:, :n]
         v = vp[idx].permute(1, 0, 3, 2).reshape(KV, nb * BLOCK, D)[:, :n]
         s = vs[idx].permute(1, 0, 2).reshape(KV, nb * BLOCK)[:, :n]
         return k, v.contiguous().view(torch.float8_e4m3fn), s.unsqueeze(-1)

@@ -61,12 +61,14 @@ def _need(t, name, dtypes, dev=None, ndim=None):
 
 def _pages_dims(k_pages, v_pages, v_scales, layered: bool):
     lead = 1 if layered else 0
-    if k_pages.dim() != 4 + lead or v_pages.dim() != 4 + lead or v_scales.dim() != 3 + lead:
-        _fail(f"page tensors must be (..., num_blocks, KV, 16, D) / (..., num_blocks, KV, D, 16) / "
+    if k_pages.dim() != 5 + lead or v_pages.dim() != 4 + lead or v_scales.dim() != 3 + lead:
+        _fail(f"page tensors must be (..., num_blocks, KV, D/8, 16, 8) / (..., num_blocks, KV, D, 16) / "
               f"(..., num_blocks, KV, 16); got {tuple(k_pages.shape)}, {tuple(v_pages.shape)}, "
               f"{tuple(v_scales.shape)}")
-    nb, kv, blk, d = k_pages.shape[lead:]
-    if blk != BLOCK or tuple(v_pages.shape[lead:]) != (nb, kv, d, BLOCK) or tuple(v_scales.shape[lead:]) != (nb, kv, BLOCK):
+    nb, kv, dc, blk, eight = k_pages.shape[lead:]
+    d = dc * 8
+    if blk != BLOCK or eight != 8 or tuple(v_pages.shape[lead:]) != (nb, kv, d, BLOCK) or \
+            tuple(v_scales.shape[lead:]) != (nb, kv, BLOCK):
         _fail(f"page shapes disagree: k {tuple(k_pages.shape)}, v {tuple(v_pages.shape)}, s {tuple(v_scales.shape)}")
     if layered and not (k_pages.shape[0] == v_pages.shape[0] == v_scales.shape[0]):
         _fail("page tensors disagree on the layer count")
@@ -101,7 +103,7 @@ def quant_append(v_new: torch.Tensor, slot_mapping: torch.Tensor, k_pages: torch
 
     v_new/k_new: BF16 (n_tokens, KV, D), or (L, n_tokens, KV, D) with layered pages.
     slot_mapping: int32 (n_tokens,), slot = block * 16 + offset, negative = skip.
-    Pages: k (…, num_blocks, KV, 16, D) BF16; v (…, num_blocks, KV, D, 16) uint8 or
+    Pages: k (…, num_blocks, KV, D/8, 16, 8) BF16; v (…, num_blocks, KV, D, 16) uint8 or
     float8_e4m3fn; scales (…, num_blocks, KV, 16) fp32.
     """
     lib = _native.load()
@@ -204,7 +206,8 @@ def pack_contiguous(k: torch.Tensor, v_payload: torch.Tensor, v_scale: torch.Ten
     vv = torch.nn.functional.pad(vv, (0, 0, 0, pad)) if pad else vv
     ss = v_scale.reshape(B, KV, T)
     ss = torch.nn.functional.pad(ss, (0, pad), value=1.0) if pad else ss
-    k_pages = kk.reshape(B, KV, nbps, BLOCK, D).permute(0, 2, 1, 3, 4).reshape(B * nbps, KV, BLOCK, D).contiguous()
+    k_pages = (kk.reshape(B, KV, nbps, BLOCK, D // 8, 8).permute(0, 2, 1, 4, 3, 5)
+               .reshape(B * nbps, KV, D // 8, BLOCK, 8).contiguous())
     v_pages = vv.reshape(B, KV, nbps, BLOCK, D).permute(0, 2, 1, 4, 3).reshape(B * nbps, KV, D, BLOCK).contiguous()
     v_scales = ss.reshape(B, KV, nbps, BLOCK).permute(0, 2, 1, 3).reshape(B * nbps, KV, BLOCK).contiguous()
     block_table = torch.arange(B * nbps, dtype=torch.int32, device=k.device).reshape(B, nbps)

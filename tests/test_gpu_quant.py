@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _pages(dev, layers, nb, kv, d):
-    k = torch.zeros((layers, nb, kv, 16, d), dtype=torch.bfloat16, device=dev)
+    k = torch.zeros((layers, nb, kv, d // 8, 16, 8), dtype=torch.bfloat16, device=dev)
     v = torch.full((layers, nb, kv, d, 16), 0xA5, dtype=torch.uint8, device=dev)  # poison
     s = torch.full((layers, nb, kv, 16), -7.0, dtype=torch.float32, device=dev)
     return k, v, s
@@ -103,8 +103,12 @@ def test_decode_appends_ragged_and_skips(cuda_device):
     got_s = vs[0].cpu().numpy()
     assert np.array_equal(got_s[written].view(np.uint32), es[written].view(np.uint32))
     assert (got_s[~written] == -7.0).all()
-    got_k = bits16(kp[0])
-    assert np.array_equal(got_k[written], ek[written])
+    got_k = bits16(kp[0])                                # (nb, kv, d/8, 16, 8)
+    blk_i, kv_i, off_i = np.nonzero(written)
+    assert np.array_equal(got_k[blk_i, kv_i, :, off_i, :], ek[blk_i, kv_i, :, off_i, :])
+    unwritten = np.ones(nb, dtype=bool)
+    unwritten[blk_i] = False
+    assert (got_k[unwritten] == 0).all()
 
 
 def test_d64_draft_shape_multi_layer(cuda_device):

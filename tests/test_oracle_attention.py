@@ -143,3 +143,14 @@ def test_golden_attention_fixture():
         qq, kk, vv = (torch.from_numpy(z[f"{name}_{x}"].view(np.int16)).view(torch.bfloat16) for x in "qkv")
         o = oatt.eager_attention(qq, kk, _vhat(vv, d))
         assert np.array_equal(_bits(o), z[f"{name}_out"]), name
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_reciprocal_scale_equals_division_for_every_bf16(d):
+    """The kernels compute bf16(s * RN(1/sqrt(D))) where eager computes bf16(s / sqrt(D))
+    (model_self.py:754) on a BF16 s; both round to the same BF16 for all 65536 inputs."""
+    x = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    fin = torch.isfinite(x.float())
+    eager = x / (d ** 0.5)                                          # the reference expression
+    kern = (x.float() * torch.tensor(1.0 / d ** 0.5, dtype=torch.float32)).to(torch.bfloat16)
+    assert torch.equal(eager.view(torch.int16)[fin], kern.view(torch.int16)[fin])

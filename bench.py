@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph-leg", action="store_true", help="skip the per-layer HIP-graph figure")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run 3 plain device copies of MIB MiB (calibrates rocprof byte counters)")
     return ap.parse_args()
 
 
@@ -83,16 +85,28 @@ def build_replicas(torch, dev, n, scattered=True):
 
 
 def time_steps(torch, step, steps, warmup, nrep):
-    for i in range(warmup):
-        step(i % nrep)
+    """Average ms per step of step(i) for i = 0..steps-1 (replica i % nrep).
+
+    The steps are captured into one HIP graph of nrep steps (one per cache replica) that is
+    replayed, so the timed region holds only GPU work: a Python call costs ~20 us of host
+    time, more than some of the kernels being timed.  HIP events bracket the replays on
+    torch's current stream, the stream the library launches on.
+    """
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(nrep):
+            step(i)
+    reps = max(1, -(-steps // nrep))
+    for _ in range(max(1, -(-warmup // nrep))):
+        graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(steps):
-        step(i % nrep)
+    for _ in range(reps):
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return e0.elapsed_time(e1) / (reps * nrep)
 
 
 def main():
@@ -141,16 +155,30 @@ def main():
     def graph_step(r):
         graphs[r].replay()
 
+    def time_graphs(steps, warmup):
+        for i in range(warmup):
+            graph_step(i % args.replicas)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            graph_step(i % args.replicas)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
     pb = phase_bytes()
     bytes_step = L * B * pb["all"]
-    main_step = multi_step if args.mode == "multi" else graph_step
-    ms = time_steps(torch, main_step, args.steps, args.warmup, args.replicas)
+    if args.mode == "multi":
+        ms = time_steps(torch, multi_step, args.steps, args.warmup, args.replicas)
+    else:
+        ms = time_graphs(args.steps, args.warmup)
     value = bytes_step / (ms * 1e-3) / 1e9
 
     # Live per-launch timing of the multi-layer call: each of the three launches timed on its
-    # own, back to back on the library's stream with HIP events (torch's current stream is the
-    # stream the library launches on).  The launches after the first reuse the workspace of
-    # the preceding full calls, so they read valid scores and statistics.
+    # own, back to back in a HIP graph, with HIP events on the library's stream.  The launches
+    # after the first reuse the workspace of the preceding full calls, so they read valid
+    # scores and statistics.
     names = {"qk": _native.PHASE_QK, "pv": _native.PHASE_PV, "reduce": _native.PHASE_REDUCE}
     per = {}
     for name, ph in names.items():
@@ -161,7 +189,7 @@ def main():
 
     graph_leg = None
     if graphs:
-        gms = time_steps(torch, graph_step, args.steps, args.warmup, args.replicas)
+        gms = time_graphs(args.steps, args.warmup)
         graph_leg = {"us_per_step": round(gms * 1e3, 2), "us_per_layer": round(gms * 1e3 / L, 3),
                      "GBps": round(bytes_step / (gms * 1e-3) / 1e9, 1),
                      "frac_of_peak": round(bytes_step / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -171,6 +199,14 @@ def main():
     tf = ROOT / "profiles" / "traffic_decode8k_multi.json"
     if tf.exists():
         traffic = json.loads(tf.read_text()).get(dom)
+
+    if args.copy_probe:
+        src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
 

@@ -199,3 +199,52 @@ class PagedKVCache:
         return {"tokens": tok, "fp8v_bytes": fp8, "bf16_bytes": bf16, "saved_frac": 1 - fp8 / max(bf16, 1),
                 "scale_frac_of_fp8v": scales / max(fp8, 1),
                 "pool_bytes": self.k_pages.numel() * 2 + self.v_pages.numel() + self.v_scales.numel() * 4}
+
+
+# ---------------------------------------------------------------------- engine layer dicts
+_ANCHORS: dict = {}
+
+
+def shape_carrier(shape, dtype, device) -> torch.Tensor:
+    """A zero-storage tensor of the given logical shape (one element, expanded).
+
+    The paged layer dict stores these under "k", "v" and "v_scale" so that code written for
+    the reference's contiguous cache -- ``cache[0]["k"].shape[2]`` for the length
+    (model_self.py:847-848, spec_cache.py:4-7), ``val[:, :, :n]`` to trim (spec_cache.py:
+    23-28), ``cache[0]["k"].device`` for new token tensors (spec_dec.py:174,185) -- keeps
+    working unchanged while the bytes live in the page pool.
+    """
+    dev = torch.device(device)
+    key = (dtype, dev)
+    anchor = _ANCHORS.get(key)
+    if anchor is None:
+        anchor = torch.zeros((), dtype=dtype, device=dev)
+        _ANCHORS[key] = anchor
+    return anchor.expand(*shape)
+
+
+class LayerPages:
+    """Handle of one engine layer's pages, carried in its cache dict under "pages"."""
+
+    def __init__(self, pool: "PagedKVCache", layer: int = 0):
+        self.pool = pool
+        self.layer = layer
+
+    def reserved_tokens(self) -> int:
+        return min(len(b) for b in self.pool.blocks) * BLOCK
+
+    def layer_dict(self, length: int) -> dict:
+        """{"fmt", "k", "v", "v_scale", "pages"} for a logical length of `length` tokens."""
+        p = self.pool
+        B, KV, D, dev = p.batch, p.kv_heads, p.head_dim, p.device
+        return {"fmt": "v_fp8",
+                "k": shape_carrier((B, KV, length, D), torch.bfloat16, dev),
+                "v": shape_carrier((B, KV, length, D), torch.float8_e4m3fn, dev),
+                "v_scale": shape_carrier((B, KV, length, 1), torch.float32, dev),
+                "pages": self}
+
+    def materialize(self, length: int) -> dict:
+        """Contiguous copies {"fmt", "k", "v", "v_scale"} in the reference's layout (for tools
+        that read the cache tensors themselves)."""
+        ks, vs, ss = zip(*(self.pool.gather(self.layer, b, length) for b in range(self.pool.batch)))
+        return {"fmt": "v_fp8", "k": torch.stack(ks), "v": torch.stack(vs), "v_scale": torch.stack(ss)}

@@ -103,6 +103,16 @@ def test_small_and_ragged_edges(cuda_device):
         assert_close(got[b], want[b], f"S=5 T={t}")
 
 
+@pytest.mark.parametrize("s,lens", [(64, [300, 64, 1000]), (77, [77]), (16, [2048])])
+def test_prefill_rows(cuda_device, s, lens):
+    """Prefill/chunked-prefill blocks: S query rows per sequence, row i sees keys j <= T-S+i
+    (model_self.py:755-764); S=77 over T=77 is a prefill from an empty cache (row 0 sees one key)."""
+    announce(f"attn prefill rows S={s} lens={lens}")
+    got, want = _run_case(cuda_device, 12, 2, 128, lens, s, seed=90 + s)
+    for b, t in enumerate(lens):
+        print("prefill", s, t, assert_close(got[b], want[b], f"S={s} T={t}"))
+
+
 def test_token_major_q_layout(cuda_device):
     announce("attn token-major q")
     got, want = _run_case(cuda_device, 12, 2, 128, [300, 777], 5, seed=72, q_token_major=True)

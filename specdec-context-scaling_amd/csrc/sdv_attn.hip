@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
       // Unconditional loads keep the wait counters exact; a missing or invalid block reads
       // block 0 (always allocated) and its tokens are masked below.
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kop[u][kk] = load_bf16x8(kp + kk * 512);
+      for (int kk = 0; kk < KK; ++kk) kop[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + kk * 512));
     }
   };
   auto compute_stage = [&](const bf16x8 (&kop)[P][KK], const int (&pbs)[P], int j0) {
@@ -258,10 +258,10 @@ __device__ __forceinline__ void pv_load(PvStage<D, NT>& st, const AttnArgs& a, i
   const int64_t page = (int64_t)(st.ok ? pb : 0) * a.KV + kvh;
   const uint8_t* vp = vlayer + (page * D + n) * kBlock;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) st.code[dt] = *reinterpret_cast<const uint4*>(vp + dt * 16 * kBlock);
-  const float4* sp = reinterpret_cast<const float4*>(slayer + page * kBlock);
+  for (int dt = 0; dt < DT; ++dt) st.code[dt] = load_stream16(vp + dt * 16 * kBlock);
+  const float* sp = slayer + page * kBlock;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) st.scl[q] = sp[q];
+  for (int q = 0; q < 4; ++q) st.scl[q] = __builtin_bit_cast(float4, load_stream16(sp + 4 * q));
   // scores of a block past the chunk stay inside the workspace row (score_stride covers it)
   const int64_t tok = (int64_t)min(st.blk, a.score_stride / kBlock - 1) * kBlock;
 #pragma unroll

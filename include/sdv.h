@@ -87,6 +87,25 @@ size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q
                                     int32_t max_seq_len);
 
 /*
+ * Zero the workspace's synchronisation area (its first SDV_SYNC_BYTES bytes) on `stream`.
+ * Call it once after allocating a workspace and before its first sdv_paged_attention; every
+ * call leaves the area zero again.  The area's first 32-bit word counts waits of the
+ * single-launch path that expired (0 unless its workgroups could not all be resident).
+ * No counterpart in the reference (it has no workspace).
+ */
+#define SDV_SYNC_BYTES 2621696
+int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Which path sdv_paged_attention takes for these sizes on the current device: the number of
+ * workgroups of the single-launch kernel, or 0 for the three-launch path (several
+ * query-row groups, or a problem the device cannot hold at once).  Queries the device's
+ * occupancy; no launch.  No counterpart in the reference.
+ */
+int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                                    int32_t q_len, int32_t head_dim, int32_t max_seq_len);
+
+/*
  * Kernels 2/3: paged GQA attention over BF16 K and FP8 V for q_len query rows per sequence
  * (q_len = 1: decode; q_len = k+1 = 5: speculative verify; any q_len >= 1 is accepted).
  *

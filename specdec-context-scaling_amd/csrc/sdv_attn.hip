@@ -28,6 +28,8 @@
 // MFMA 16x16x32 lane layout (measured on gfx950): A lane l supplies row l%16, B lane l
 // supplies column l%16, both with the same 8 k-slots for lane group l/16; the result lane
 // l holds rows 4*(l/16)+i, column l%16.  Every operand below uses that mapping.
+#include <atomic>
+
 #include "sdv_internal.h"
 
 namespace sdv {
@@ -47,6 +49,10 @@ struct AttnArgs {
   uint16_t* scores;
   float2* stats;
   float* partial;
+  unsigned* sync;   // fused path: expired-wait count, tickets, published statistics (zero between calls)
+  float* fpart;     // fused path: per-item fp32 partial outputs
+  int64_t fpart_bytes;
+  int f_gb, f_base, f_extra, f_maxblk;  // fused: blocks per group, items per group (+1 for the first f_extra groups), LDS width
   int64_t q_ls, q_sb, q_sh, q_ss;  // element strides of q/out: layer, batch, head, row
   int max_blocks, num_blocks, max_seq_len;
   int B, KV, S, G, R;
@@ -231,17 +237,23 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------- p.V
 // One PV pipeline stage: 4 page blocks (64 tokens) of one wavefront.  Lane (g, n) owns block
 // g of the stage: all 16 tokens of V dimension dt*16+n (one 16-byte load per dimension
-// tile; the V page is dimension-major), the 16 scales of the block, and the 16 BF16 scores
-// of its query row n.  The MFMA k-slots of lane group g are tokens 8h..8h+7 of block g,
-// for the two token halves h.
+// tile; the V page is dimension-major), the scale of token n of the block, and the 16 BF16
+// scores of its query row n.  The MFMA k-slots of lane group g are tokens 8h..8h+7 of block
+// g, for the two token halves h.
 template <int D, int NT>
 struct PvStage {
   uint4 code[D / 16];  // E4M3FN codes, token i of the block in byte i
-  float4 scl[4];       // per-token scales
+  float scl;           // scale of token n of block g (the row broadcast hands it to the lane group)
   uint4 sc[NT][2];     // BF16 scores, tokens 0..7 and 8..15
   int blk;             // block index within the sequence (this lane group's)
   bool ok;             // the block exists and its page id is valid
 };
+
+// value of lane I of this lane's 16-lane row (DPP row_newbcast)
+template <int I>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + I, 0xF, 0xF, false));
+}
 
 template <int D, int NT>
 __device__ __forceinline__ void pv_load(PvStage<D, NT>& st, const AttnArgs& a, int j, int my_pb, int nb, int blk0,
@@ -259,9 +271,7 @@ __device__ __forceinline__ void pv_load(PvStage<D, NT>& st, const AttnArgs& a, i
   const uint8_t* vp = vlayer + (page * D + n) * kBlock;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) st.code[dt] = load_stream16(vp + dt * 16 * kBlock);
-  const float* sp = slayer + page * kBlock;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) st.scl[q] = __builtin_bit_cast(float4, load_stream16(sp + 4 * q));
+  st.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
   // scores of a block past the chunk stay inside the workspace row (score_stride covers it)
   const int64_t tok = (int64_t)min(st.blk, a.score_stride / kBlock - 1) * kBlock;
 #pragma unroll
@@ -272,9 +282,54 @@ __device__ __forceinline__ void pv_load(PvStage<D, NT>& st, const AttnArgs& a, i
   }
 }
 
+// One token half (tokens 8H..8H+7 of each lane group's block) of a stage on the MFMA.
+template <int D, int NT, int H>
+__device__ __forceinline__ void pv_half(const PvStage<D, NT>& st, f32x4 (&acc)[D / 16][NT], const float (&gm)[NT],
+                                        const float (&ginv)[NT]) {
+  constexpr int DT = D / 16;
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  // P^T operand (B): probabilities of this lane's row for tokens 8H..8H+7 of its block.
+  bf16x8 pop[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const uint4 w4 = st.sc[nt][H];
+    const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
+    float pr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float s = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
+      pr[i] = fast_exp(s - gm[nt]) * ginv[nt];  // -inf score -> 0
+    }
+    pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                                    pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+  }
+  // per-token scales of tokens 8H..8H+7 of this lane group's block
+  const float s0 = row_bcast<8 * H + 0>(st.scl), s1 = row_bcast<8 * H + 1>(st.scl);
+  const float s2 = row_bcast<8 * H + 2>(st.scl), s3 = row_bcast<8 * H + 3>(st.scl);
+  const float s4 = row_bcast<8 * H + 4>(st.scl), s5 = row_bcast<8 * H + 5>(st.scl);
+  const float s6 = row_bcast<8 * H + 6>(st.scl), s7 = row_bcast<8 * H + 7>(st.scl);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    // V_hat^T operand (A): dimension dt*16+n, tokens 8H..8H+7 of this lane group's block,
+    // each bf16(f32(code) * scale) as dequantize_kv_fp8 rounds it.
+    const uint32_t lo = H ? st.code[dt].z : st.code[dt].x;
+    const uint32_t hi = H ? st.code[dt].w : st.code[dt].y;
+    const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+    const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+    const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+    const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    const bf16x8 vop = __builtin_bit_cast(
+        bf16x8, make_uint4(pack_bf16x2(f01.x * s0, f01.y * s1), pack_bf16x2(f23.x * s2, f23.y * s3),
+                           pack_bf16x2(f45.x * s4, f45.y * s5), pack_bf16x2(f67.x * s6, f67.y * s7)));
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+      acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dt][nt], 0, 0, 0);
+  }
+}
+
 template <int D, int NT>
 __device__ __forceinline__ void pv_compute(PvStage<D, NT>& st, f32x4 (&acc)[D / 16][NT], const float (&gm)[NT],
-                                           const float (&ginv)[NT], int T, bool stage_full) {
+                                           const float (&ginv)[NT], int T, bool stage_full, int n) {
   constexpr int DT = D / 16;
   // wave-uniform: every block of the stage exists, has a valid page and lies below T
   if (!stage_full || __ballot(!st.ok) != 0) {
@@ -294,9 +349,7 @@ __device__ __forceinline__ void pv_compute(PvStage<D, NT>& st, f32x4 (&acc)[D / 
       st.code[dt].z &= bmask[2];
       st.code[dt].w &= bmask[3];
     }
-    float* sf = reinterpret_cast<float*>(st.scl);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) sf[i] = i < nvalid ? sf[i] : 0.0f;
+    st.scl = n < nvalid ? st.scl : 0.0f;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       uint32_t* sw = reinterpret_cast<uint32_t*>(st.sc[nt]);
@@ -307,52 +360,17 @@ __device__ __forceinline__ void pv_compute(PvStage<D, NT>& st, f32x4 (&acc)[D / 
       }
     }
   }
-  const float* sf = reinterpret_cast<const float*>(st.scl);
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    // P^T operand (B): probabilities of this lane's row for tokens 8h..8h+7 of its block.
-    bf16x8 pop[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const uint4 w4 = st.sc[nt][h];
-      const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
-      float pr[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float s = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
-        pr[i] = fast_exp(s - gm[nt]) * ginv[nt];  // -inf score -> 0
-      }
-      pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                                                      pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
-    }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      // V_hat^T operand (A): dimension dt*16+n, tokens 8h..8h+7 of this lane group's block.
-      typedef float f32x2 __attribute__((ext_vector_type(2)));
-      const uint32_t lo = h ? st.code[dt].z : st.code[dt].x;
-      const uint32_t hi = h ? st.code[dt].w : st.code[dt].y;
-      const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
-      const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-      const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
-      const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-      const float* sc = sf + 8 * h;
-      const bf16x8 vop = __builtin_bit_cast(
-          bf16x8, make_uint4(pack_bf16x2(f01.x * sc[0], f01.y * sc[1]), pack_bf16x2(f23.x * sc[2], f23.y * sc[3]),
-                             pack_bf16x2(f45.x * sc[4], f45.y * sc[5]), pack_bf16x2(f67.x * sc[6], f67.y * sc[7])));
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dt][nt], 0, 0, 0);
-    }
-  }
+  pv_half<D, NT, 0>(st, acc, gm, ginv);
+  pv_half<D, NT, 1>(st, acc, gm, ginv);
 }
 
+#ifndef SDV_PV_WAVES_PER_EU  // tuning builds: occupancy floor the compiler must fit pv_kernel into
+#define SDV_PV_WAVES_PER_EU 1
+#endif
 template <int D, int NT>
-__global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SDV_PV_WAVES_PER_EU))) void pv_kernel(AttnArgs a) {
   constexpr int DT = D / 16;  // 16-dimension MFMA tiles
   constexpr int RT = NT * 16;
-  constexpr int SLICES = 256 / RT;
-  __shared__ float2 lstat[SLICES * RT];
-  __shared__ float2 lms[RT];
   __shared__ float lacc[kWaves][16][D + 4];  // +4: spread the lane groups over LDS banks
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int c = blockIdx.x;
@@ -367,6 +385,34 @@ __global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
   const int nb = max(0, min(a.pv_bpw, ((T + kBlock - 1) >> 4) - blk0));
   int my_pb = -1;
   if (lane < nb) my_pb = a.block_table[(int64_t)b * a.max_blocks + blk0 + lane];
+
+  // Chunk statistics of this lane's query rows, issued before the V loads so that waiting
+  // for them leaves V in flight.  Lane group g merges chunks g, g+4, ... in order.
+  const int nvq = (T + a.qk_chunk_tokens - 1) / a.qk_chunk_tokens;
+  float sm[NT], sl[NT];
+  {
+    const float2* st0 = a.stats + (int64_t)grp * a.n_qk_chunks * a.rpad;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int rr = rg * RT + nt * 16 + n;
+      const float2* st = st0 + (rr < a.R ? rr : 0);
+      float m = -INFINITY, l = 0.0f;
+      int cc = g;
+      for (; cc + 12 < nvq; cc += 16) {
+        float2 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = st[(int64_t)(cc + 4 * u) * a.rpad];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) merge_fast(m, l, v[u].x, v[u].y);
+      }
+      for (; cc < nvq; cc += 4) {
+        const float2 v = st[(int64_t)cc * a.rpad];
+        merge_fast(m, l, v.x, v.y);
+      }
+      sm[nt] = m;
+      sl[nt] = l;
+    }
+  }
   if (my_pb >= a.num_blocks) my_pb = -1;
 
   // score rows of this lane's query row in each row tile (padding rows read row 0; their
@@ -381,47 +427,24 @@ __global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
   const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
   const float* slayer = a.v_scales + layer * a.s_ls;
 
-  // Stage 0 of V is in flight while the statistics below are merged.
+  // Stages 0 and 1 of V are in flight while the statistics are merged.  The prefetch is
+  // unconditional (a stage past the end reads block 0 and is never computed) so the wait
+  // counters stay exact.
   const int nst = (nb + 3) >> 2;
   PvStage<D, NT> sa, sb;
-  if (nst > 0) pv_load<D, NT>(sa, a, 0, my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
+  pv_load<D, NT>(sa, a, 0, my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
+  pv_load<D, NT>(sb, a, 4, my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
 
-  // --- global softmax statistics of this row group: thread (slice, row) merges chunks
-  // slice, slice+SLICES, ...; slices then merge in order.  Fixed order: deterministic.
-  {
-    const int r = tid % RT, slice = tid / RT;
-    const int nvq = (T + a.qk_chunk_tokens - 1) / a.qk_chunk_tokens;
-    float m = -INFINITY, l = 0.0f;
-    const int srow = rg * RT + r;
-    if (slice < SLICES && srow < a.R) {
-      const float2* st = a.stats + (int64_t)grp * a.n_qk_chunks * a.rpad + srow;
-      int cc = slice;
-      for (; cc + 3 * SLICES < nvq; cc += 4 * SLICES) {
-        float2 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = st[(int64_t)(cc + u * SLICES) * a.rpad];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) merge_fast(m, l, v[u].x, v[u].y);
-      }
-      for (; cc < nvq; cc += SLICES) {
-        const float2 v = st[(int64_t)cc * a.rpad];
-        merge_fast(m, l, v.x, v.y);
-      }
-    }
-    if (slice < SLICES) lstat[slice * RT + r] = make_float2(m, l);
-    __syncthreads();
-    if (tid < RT) {
-      float mm = lstat[tid].x, ll = lstat[tid].y;
-      for (int s2 = 1; s2 < SLICES; ++s2) merge_fast(mm, ll, lstat[s2 * RT + tid].x, lstat[s2 * RT + tid].y);
-      lms[tid] = make_float2(mm, 1.0f / ll);
-    }
-    __syncthreads();
-  }
+  // global (M, 1/L) of each row: the four lane groups' partial merges combine in a fixed
+  // tree (xor 16, then xor 32), so every lane, wave and workgroup gets identical values.
   float gm[NT], ginv[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    gm[nt] = lms[nt * 16 + n].x;
-    ginv[nt] = lms[nt * 16 + n].y;
+    float m = sm[nt], l = sl[nt];
+    merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
+    merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+    gm[nt] = m;
+    ginv[nt] = 1.0f / l;
   }
 
   f32x4 acc[DT][NT];
@@ -430,18 +453,16 @@ __global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Ping-pong over stages; the prefetch is unconditional (a stage past the end reads block
-  // 0 and is masked) so the wait counters stay exact.  A stage is "full" (no masking) when
-  // all 64 of its slots are tokens of the sequence -- wave-uniform.
+  // Ping-pong over stages.  A stage is "full" (no masking) when all 64 of its slots are
+  // tokens of the sequence -- wave-uniform.
   const int full_stages = min(nb, max(0, (T >> 4) - blk0)) >> 2;
-  int st_i = 0;
-  for (; st_i + 1 < nst; st_i += 2) {
-    pv_load<D, NT>(sb, a, 4 * (st_i + 1), my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
-    pv_compute<D, NT>(sa, acc, gm, ginv, T, st_i < full_stages);
+  for (int st_i = 0; st_i < nst; st_i += 2) {
+    pv_compute<D, NT>(sa, acc, gm, ginv, T, st_i < full_stages, n);
+    if (st_i + 1 >= nst) break;
     pv_load<D, NT>(sa, a, 4 * (st_i + 2), my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
-    pv_compute<D, NT>(sb, acc, gm, ginv, T, st_i + 1 < full_stages);
+    pv_compute<D, NT>(sb, acc, gm, ginv, T, st_i + 1 < full_stages, n);
+    pv_load<D, NT>(sb, a, 4 * (st_i + 3), my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
   }
-  if (st_i < nst) pv_compute<D, NT>(sa, acc, gm, ginv, T, st_i < full_stages);
 
   // lane (g, n) holds O^T[dims dt*16 + 4g .. +3][row n]; the 4 waves sum in LDS per row tile.
   float* dst = a.partial + ((int64_t)grp * a.n_pv_chunks + c) * a.R * D;
@@ -500,13 +521,613 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------- fused
+// One launch for the shapes whose whole grid fits the device at once (one query-row group:
+// decode and verify).  One workgroup per CU (W = 16 wavefronts for decode; 8 or 4 when the
+// row tiles need more registers), each owning one item: a run of page blocks of one
+// (layer*batch, KV head) group.  Groups are cut into items of nearly equal size (a group
+// gets f_base or f_base+1 items), so every CU streams the same number of bytes.  Inside a
+// workgroup the wavefronts claim page blocks from an LDS counter, so a wavefront the
+// scheduler favours takes more blocks and all finish together.  Per workgroup:
+//   1. q.k^T over the item's blocks: BF16 scores and per-block (max, sum) of every row into
+//      LDS; the item's (max, sum) -- merged over its blocks in block order, so it does not
+//      depend on which wavefront took which block -- published to device memory.  A
+//      published entry is never all-zero bits (sum >= 1, or max = -inf), so zero means "not
+//      yet": no counter is needed for this step.
+//   2. Once every non-empty item of the group has published, the group's statistics are
+//      merged in a fixed order; each wavefront runs p.V for one 16-dimension tile (or more)
+//      and one part of the item's blocks; parts are summed in LDS in order and the fp32
+//      partial is published.
+//   3. Every workgroup of the group takes a ticket, waits until all partials are published,
+//      and sums its slice of the outputs over the items in order (the result does not
+//      depend on the order workgroups finish) into the BF16 output; the last one past the
+//      wait zeroes the group's entries and counters for the next call.
+// Cross-workgroup data moves through device-scope (sc1) stores and loads, which bypass the
+// per-XCD L2 caches; `s_waitcnt vmcnt(0)` before the ticket orders the partial ahead of it.
+// No cache-writeback fence is issued (on gfx950 each agent-scope release costs ~40 ns and
+// serialises chip-wide).  Deadlock freedom: a workgroup publishes before it waits and the
+// grid never exceeds the device's resident capacity (occupancy query), so every entry a
+// wait needs comes from a running workgroup.  Waits are bounded; on expiry they count an
+// error in word 0 of the synchronisation area and continue.
+constexpr int kFusedMaxGroups = 4096;   // tickets in the synchronisation area
+constexpr int kFusedMaxItems = 4096;    // published (max, sum) rows: 64 per item
+constexpr int kFusedMaxChunks = 64;     // items per group
+constexpr size_t kSyncTicketWords = 64 + (size_t)kFusedMaxGroups * 32;  // tickets 128 bytes apart
+constexpr size_t kSyncBytes = kSyncTicketWords * 4 + (size_t)kFusedMaxItems * 64 * 8;
+static_assert(kSyncBytes == SDV_SYNC_BYTES, "sdv.h states the synchronisation prefix size");
+
+#define SDV_VMCNT0() __builtin_amdgcn_s_waitcnt(0x0F70)  // vmcnt(0); exp/lgkm counters untouched
+
+__device__ __forceinline__ void store_dev_f2(float2* p, float2 v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_dev_u64(const float2* p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2* sync_stats(const AttnArgs& a) {
+  return reinterpret_cast<float2*>(a.sync + kSyncTicketWords);
+}
+__device__ __forceinline__ unsigned* sync_ticket(const AttnArgs& a, int grp) { return a.sync + 64 + grp * 32; }
+
+// wavefronts of the fused workgroup for NT row tiles
+template <int NT>
+constexpr int fused_waves() { return NT == 1 ? 16 : NT == 2 ? 8 : 4; }
+constexpr int kVStages = 6;  // p.V stages in flight per wavefront
+
+// dynamic LDS of a fused workgroup with items of up to `maxblk` blocks (byte offsets).  With
+// one row tile the p.V work is claimed in units and each unit's result gets an LDS slot
+// ([stage][R][D] floats); otherwise the parts of the static split ([parts][R][D]).
+struct FusedLds {
+  int scores, bstats, pages, parts, total;
+};
+__host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool claim_pv) {
+  const int DT = D / 16, ntg = DT < W ? DT : W, tp = W / ntg;
+  FusedLds l;
+  l.scores = 0;                                                            // [R][16*maxblk + 8] bf16
+  l.bstats = (l.scores + R * (maxblk * kBlock + 8) * 2 + 15) & ~15;        // [maxblk][R] float2
+  l.pages = l.bstats + maxblk * R * 8;                                     // [maxblk] int
+  l.parts = (l.pages + maxblk * 4 + 15) & ~15;
+  l.total = l.parts + (claim_pv ? (maxblk + 3) / 4 : (tp > 1 ? tp : 0)) * R * D * 4;
+  return l;
+}
+
+template <int D, int NT>
+__global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs a) {
+  constexpr int W = fused_waves<NT>(), NTHR = 64 * W;
+  constexpr int KK = D / 32, DT = D / 16;
+  constexpr int NTG = DT < W ? DT : W;   // dimension-tile groups in p.V
+  constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
+  constexpr int TP = W / NTG;            // block parts in p.V
+  constexpr int P = 2;                   // page blocks per q.k^T claim
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  extern __shared__ uint4 smem_u4[];
+  __shared__ int s_next, s_next2, s_last;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int item = blockIdx.x;
+  const int big = a.f_extra * (a.f_base + 1);  // workgroups of the groups with one more item
+  int grp, c, n_g, item0;
+  if (item < big) {
+    n_g = a.f_base + 1;
+    grp = item / n_g;
+    c = item - grp * n_g;
+    item0 = grp * n_g;
+  } else {
+    n_g = a.f_base;
+    const int q = (item - big) / n_g;
+    grp = a.f_extra + q;
+    c = item - big - q * n_g;
+    item0 = big + q * n_g;
+  }
+  const int blk_lo = (int)((int64_t)c * a.f_gb / n_g);
+  const int nbk = (int)((int64_t)(c + 1) * a.f_gb / n_g) - blk_lo;  // item blocks, 1..f_maxblk
+  const int zb = grp / a.KV, kvh = grp - zb * a.KV, b = zb % a.B, layer = zb / a.B;
+  const int T = seq_len_of(a, b);
+  const int tok0 = blk_lo * kBlock;
+  if (tok0 >= T) {
+    if (T == 0 && c == 0) {  // empty sequence: the eager sum over no keys is 0
+      for (int o = tid; o < a.R * D; o += NTHR) {
+        const int row = o / D, d = o - row * D, hl = row / a.S, si = row % a.S;
+        a.out[layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d] = 0;
+      }
+    }
+    return;  // workgroup-uniform
+  }
+  const int nblk_seq = (T + kBlock - 1) >> 4;
+  const int nbv = min(nbk, nblk_seq - blk_lo);  // item blocks inside the sequence (>= 1)
+  // non-empty items of the group: item i starts at block floor(i * gb / n_g)
+  const int nvq = min(n_g, (int)(((int64_t)nblk_seq * n_g + a.f_gb - 1) / a.f_gb));
+
+  constexpr bool kClaimPV = NT == 1;  // one row tile: p.V units claimed like q.k^T blocks
+  const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kClaimPV);
+  char* smem = reinterpret_cast<char*>(smem_u4);
+  uint16_t* lsc = reinterpret_cast<uint16_t*>(smem + lay.scores);  // row r: scores of query row r
+  const int lrow = a.f_maxblk * kBlock + 8;
+  float2* bst = reinterpret_cast<float2*>(smem + lay.bstats);      // [block][row] (max, sum)
+  int* lpb = reinterpret_cast<int*>(smem + lay.pages);              // page ids of the item blocks
+  const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
+  for (int j = tid; j < nbv; j += NTHR) {
+    const int pb = btrow[blk_lo + j];
+    lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
+  }
+  if (tid == 0) s_next = s_next2 = 0;
+  __syncthreads();
+
+  // ------------------------------------------------------------------ 1. q.k^T
+  bf16x8 qop[NT][KK];
+  int qsi[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = nt * 16 + n;
+    const bool rv = row < a.R;
+    const int hl = rv ? row / a.S : 0;
+    qsi[nt] = rv ? row % a.S : 0;
+    const uint16_t* qp =
+        a.q + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + qsi[nt] * a.q_ss + g * 8;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qop[nt][kk] = rv ? load_bf16x8(qp + kk * 32) : zero_bf16x8();
+  }
+  {
+    const uint16_t* kbase = a.k_pages + layer * a.k_ls + (int64_t)lane * 8;
+    // claim P blocks; returns the first (wave-uniform), >= nbv when the item is exhausted
+    auto claim = [&]() -> int {
+      int j = 0;
+      if (lane == 0) j = atomicAdd(&s_next, P);
+      return __builtin_amdgcn_readfirstlane(j);
+    };
+    auto load_stage = [&](int j0, bf16x8 (&kop)[P][KK], int (&pbs)[P]) {
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        pbs[u] = (j0 + u < nbv) ? lpb[j0 + u] : -1;
+        const uint16_t* kp = kbase + ((int64_t)max(pbs[u], 0) * a.KV + kvh) * (kBlock * D);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) kop[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + kk * 512));
+      }
+    };
+    auto compute_stage = [&](const bf16x8 (&kop)[P][KK], const int (&pbs)[P], int j0) {
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        const int jb = j0 + u;  // block within the item
+        if (jb >= nbv) break;
+        const int tb = tok0 + jb * kBlock + 4 * g;  // this lane's first token
+        const bool blk_ok = pbs[u] >= 0;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[u][kk], qop[nt][kk], acc, 0, 0, 0);
+          float s4[4];
+          float mt = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = tb + i;
+            const float x = round_bf16(round_bf16(acc[i]) * a.inv_sqrt_d);
+            const bool vis = blk_ok && t < T && t <= T - a.S + qsi[nt];
+            s4[i] = vis ? x : -INFINITY;
+            mt = fmaxf(mt, s4[i]);
+          }
+          const int row = nt * 16 + n;
+          if (row < a.R)
+            *reinterpret_cast<uint2*>(lsc + row * lrow + jb * kBlock + 4 * g) =
+                make_uint2(pack_bf16x2(s4[0], s4[1]), pack_bf16x2(s4[2], s4[3]));
+          // this block's (max, sum) of the row: the four lane groups combine in a fixed tree
+          float l = 0.0f;
+          if (mt != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) l += fast_exp(s4[i] - mt);
+          }
+          float m = mt;
+          merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
+          merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+          if (g == 0 && row < a.R) bst[jb * a.R + row] = make_float2(m, l);
+        }
+      }
+    };
+    bf16x8 ka[P][KK], kb[P][KK];
+    int pa[P], pbb[P];
+    int ja = claim();
+    load_stage(ja, ka, pa);
+    while (ja < nbv) {
+      const int jb2 = claim();
+      load_stage(jb2, kb, pbb);
+      compute_stage(ka, pa, ja);
+      if (jb2 >= nbv) break;
+      ja = claim();
+      load_stage(ja, ka, pa);
+      compute_stage(kb, pbb, jb2);
+    }
+  }
+  __syncthreads();
+  float2* fs = sync_stats(a);
+  // the item's statistics of each row: lane l merges blocks l, l+64, ... in order, then a
+  // fixed xor tree over the 64 lanes -- independent of which wavefront took which block
+  for (int row = wave; row < a.R; row += W) {
+    float m = -INFINITY, l = 0.0f;
+    for (int j = lane; j < nbv; j += kWave) {
+      const float2 v = bst[j * a.R + row];
+      merge_fast(m, l, v.x, v.y);
+    }
+#pragma unroll
+    for (int x = 1; x < kWave; x <<= 1) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));
+    if (lane == 0) store_dev_f2(fs + (int64_t)item * 64 + row, make_float2(m, l));
+  }
+
+  // ------------------------------------------------------------------ 2. p.V
+  const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
+  const float* slayer = a.v_scales + layer * a.s_ls;
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(a.fpart, (short)0, (int)a.fpart_bytes, 0x00020000);
+  const int64_t pstride = (int64_t)a.R * D;  // floats per item
+  float* lparts = reinterpret_cast<float*>(smem + lay.parts);
+  // the group's statistics: wait until all nvq items have published (each wavefront on its
+  // own), then merge in a fixed order -- lane group g takes items g, g+4, ..., then the xor
+  // tree -- so every lane, wavefront and workgroup of the group gets identical values
+  auto group_stats = [&](float (&gm)[NT], float (&ginv)[NT]) {
+    const int ne = (nvq - g + 3) >> 2;  // items of this lane group
+    const int ne_max = (nvq + 3) >> 2;  // wave-uniform loop bound
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int rr = nt * 16 + n;
+      const float2* fp = fs + (int64_t)item0 * 64 + (rr < a.R ? rr : 0);
+      float m = -INFINITY, l = 0.0f;
+      for (int k0 = 0; k0 < ne_max; k0 += 8) {
+        uint64_t e[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) e[k] = k0 + k < ne ? load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64) : 1;
+        unsigned spins = 0;
+        for (;;) {
+          bool ready = true;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) ready = ready && e[k] != 0;
+          if (__ballot(!ready) == 0) break;
+          if (++spins > (1u << 20)) {
+            if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (e[k] == 0) e[k] = load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (k0 + k < ne) {
+            const float2 v = __builtin_bit_cast(float2, e[k]);
+            merge_fast(m, l, v.x, v.y);
+          }
+        }
+      }
+      merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
+      merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+      gm[nt] = m;
+      ginv[nt] = 1.0f / l;
+    }
+  };
+
+  float gm[NT], ginv[NT];
+  if constexpr (kClaimPV) {
+    // Units of (4 blocks, up to 4 dimension tiles), claimed from an LDS counter so that all
+    // wavefronts finish together.  Each unit's fp32 result goes to its own LDS slot and the
+    // slots are summed in stage order, so the partial does not depend on who took what.
+    constexpr int UT = DT < 4 ? DT : 4;  // 16-dimension tiles per unit
+    constexpr int NH = DT / UT;          // units per stage of 4 blocks
+    const int nstage = (nbv + 3) >> 2;
+    const int nunits = nstage * NH;
+    struct Unit {
+      uint4 code[UT];
+      float scl;
+      int nvalid;
+    };
+    auto claim2 = [&]() -> int {
+      int j = 0;
+      if (lane == 0) j = atomicAdd(&s_next2, 1);
+      return __builtin_amdgcn_readfirstlane(j);
+    };
+    // a unit past the end reads block 0 (the wait counters stay exact) and is never computed
+    auto load_u = [&](int u, Unit& x) {
+      const int k = u / NH, hf = u - k * NH;
+      const int jb = 4 * k + g;
+      const int pb = (u < nunits && jb < nbv) ? lpb[jb] : -1;
+      x.nvalid = pb >= 0 ? min(max(T - (tok0 + jb * kBlock), 0), kBlock) : 0;
+      const int64_t page = (int64_t)(x.nvalid > 0 ? pb : 0) * a.KV + kvh;
+      const uint8_t* vp = vlayer + (page * D + hf * UT * 16 + n) * kBlock;
+#pragma unroll
+      for (int t = 0; t < UT; ++t) x.code[t] = load_stream16(vp + t * 16 * kBlock);
+      x.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
+    };
+    auto compute_u = [&](int u, Unit& x) {
+      const int k = u / NH, hf = u - k * NH;
+      const int jb = 4 * k + g;
+      if (__ballot(x.nvalid < kBlock) != 0) {  // wave-uniform: sanitize slots that are not tokens
+        uint32_t bmask[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int kk2 = min(max(x.nvalid - 4 * w, 0), 4);
+          bmask[w] = kk2 >= 4 ? 0xFFFFFFFFu : ((1u << (8 * kk2)) - 1u);
+        }
+#pragma unroll
+        for (int t = 0; t < UT; ++t) {
+          x.code[t].x &= bmask[0];
+          x.code[t].y &= bmask[1];
+          x.code[t].z &= bmask[2];
+          x.code[t].w &= bmask[3];
+        }
+        x.scl = n < x.nvalid ? x.scl : 0.0f;
+      }
+      f32x4 acc[UT];
+#pragma unroll
+      for (int t = 0; t < UT; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // rows past R and lane groups past the item see -inf scores: p = 0, never inf * 0
+        uint4 w4 = make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u);
+        if (jb < nbv && n < a.R) w4 = *reinterpret_cast<const uint4*>(lsc + n * lrow + jb * kBlock + 8 * h);
+        const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
+          pr[i] = fast_exp(sc - gm[0]) * ginv[0];
+        }
+        const bf16x8 pop = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                                                 pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+        float sv[8];
+        if (h == 0) {
+          sv[0] = row_bcast<0>(x.scl); sv[1] = row_bcast<1>(x.scl); sv[2] = row_bcast<2>(x.scl);
+          sv[3] = row_bcast<3>(x.scl); sv[4] = row_bcast<4>(x.scl); sv[5] = row_bcast<5>(x.scl);
+          sv[6] = row_bcast<6>(x.scl); sv[7] = row_bcast<7>(x.scl);
+        } else {
+          sv[0] = row_bcast<8>(x.scl); sv[1] = row_bcast<9>(x.scl); sv[2] = row_bcast<10>(x.scl);
+          sv[3] = row_bcast<11>(x.scl); sv[4] = row_bcast<12>(x.scl); sv[5] = row_bcast<13>(x.scl);
+          sv[6] = row_bcast<14>(x.scl); sv[7] = row_bcast<15>(x.scl);
+        }
+#pragma unroll
+        for (int t = 0; t < UT; ++t) {
+          const uint32_t lo = h ? x.code[t].z : x.code[t].x;
+          const uint32_t hi = h ? x.code[t].w : x.code[t].y;
+          const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+          const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+          const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+          const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+          const bf16x8 vop = __builtin_bit_cast(
+              bf16x8, make_uint4(pack_bf16x2(f01.x * sv[0], f01.y * sv[1]), pack_bf16x2(f23.x * sv[2], f23.y * sv[3]),
+                                 pack_bf16x2(f45.x * sv[4], f45.y * sv[5]), pack_bf16x2(f67.x * sv[6], f67.y * sv[7])));
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[t], 0, 0, 0);
+        }
+      }
+      // lane (g, n) holds row n, dims hf*UT*16 + t*16 + 4g .. +3 of stage k
+      if (n < a.R) {
+#pragma unroll
+        for (int t = 0; t < UT; ++t)
+          *reinterpret_cast<f32x4*>(lparts + ((k * a.R + n) * D + hf * UT * 16 + t * 16 + 4 * g)) = acc[t];
+      }
+    };
+    Unit ua, ub;
+    int u0 = claim2();
+    load_u(u0, ua);
+    group_stats(gm, ginv);
+    while (u0 < nunits) {
+      const int u1 = claim2();
+      load_u(u1, ub);
+      compute_u(u0, ua);
+      if (u1 >= nunits) break;
+      u0 = claim2();
+      load_u(u0, ua);
+      compute_u(u1, ub);
+    }
+    __syncthreads();
+    // the item's partial: unit slots summed in stage order
+    for (int o4 = tid; o4 * 4 < a.R * D; o4 += NTHR) {
+      f32x4 v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k = 0; k < nstage; ++k) v += *reinterpret_cast<const f32x4*>(lparts + k * a.R * D + 4 * o4);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
+    }
+  } else {
+    // wavefront (tile group tg, part pt): dims [tg*DTW*16, +DTW*16), blocks [pbeg, pend)
+    const int tg = wave % NTG, pt = wave / NTG;
+    const int pbeg = (nbv * pt) / TP, pend = (nbv * (pt + 1)) / TP;
+    const int nstage = (pend - pbeg + 3) >> 2;  // 4 blocks per stage (lane group g: block 4*st + g)
+    struct Stage {
+      uint4 code[DTW];
+      float scl;
+      int nvalid;
+    };
+    auto load_v = [&](int st, Stage& s) {
+      const int jb = pbeg + 4 * st + g;
+      const int pb = jb < pend ? lpb[min(jb, nbv - 1)] : -1;
+      s.nvalid = pb >= 0 ? min(max(T - (tok0 + jb * kBlock), 0), kBlock) : 0;
+      const int64_t page = (int64_t)(s.nvalid > 0 ? pb : 0) * a.KV + kvh;
+      const uint8_t* vp = vlayer + (page * D + tg * DTW * 16 + n) * kBlock;
+  #pragma unroll
+      for (int dtw = 0; dtw < DTW; ++dtw) s.code[dtw] = load_stream16(vp + dtw * 16 * kBlock);
+      s.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
+    };
+    // kVStages stages of V in flight per wavefront: a stage is only 1 KiB of codes per 16-dim
+    // tile, so a deep ring keeps enough bytes moving; loads past the end read block 0 (the
+    // wait counters stay exact) and are never computed
+    constexpr int SD = kVStages;
+    Stage ring[SD];
+  #pragma unroll
+    for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
+
+    group_stats(gm, ginv);
+    f32x4 acc[DTW][NT];
+  #pragma unroll
+    for (int dtw = 0; dtw < DTW; ++dtw)
+  #pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[dtw][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute_v = [&](int st, Stage& s) {
+      const int jb = pbeg + 4 * st + g;
+      const bool in_part = jb < pend;
+      if (__ballot(s.nvalid < kBlock) != 0) {  // wave-uniform: sanitize slots that are not tokens
+        uint32_t bmask[4];
+  #pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const int k = min(max(s.nvalid - 4 * w, 0), 4);
+          bmask[w] = k >= 4 ? 0xFFFFFFFFu : ((1u << (8 * k)) - 1u);
+        }
+  #pragma unroll
+        for (int dtw = 0; dtw < DTW; ++dtw) {
+          s.code[dtw].x &= bmask[0];
+          s.code[dtw].y &= bmask[1];
+          s.code[dtw].z &= bmask[2];
+          s.code[dtw].w &= bmask[3];
+        }
+        s.scl = n < s.nvalid ? s.scl : 0.0f;
+      }
+  #pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        bf16x8 pop[NT];
+  #pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          // rows past R and lane groups past the part see -inf scores: p = 0, never inf * 0
+          const int row = nt * 16 + n;
+          uint4 w4 = make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u);
+          if (in_part && row < a.R) w4 = *reinterpret_cast<const uint4*>(lsc + row * lrow + jb * kBlock + 8 * h);
+          const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
+          float pr[8];
+  #pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
+            pr[i] = fast_exp(sc - gm[nt]) * ginv[nt];  // masked (-inf) scores -> 0
+          }
+          pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                                          pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+        }
+        float sv[8];
+        if (h == 0) {
+          sv[0] = row_bcast<0>(s.scl); sv[1] = row_bcast<1>(s.scl); sv[2] = row_bcast<2>(s.scl);
+          sv[3] = row_bcast<3>(s.scl); sv[4] = row_bcast<4>(s.scl); sv[5] = row_bcast<5>(s.scl);
+          sv[6] = row_bcast<6>(s.scl); sv[7] = row_bcast<7>(s.scl);
+        } else {
+          sv[0] = row_bcast<8>(s.scl); sv[1] = row_bcast<9>(s.scl); sv[2] = row_bcast<10>(s.scl);
+          sv[3] = row_bcast<11>(s.scl); sv[4] = row_bcast<12>(s.scl); sv[5] = row_bcast<13>(s.scl);
+          sv[6] = row_bcast<14>(s.scl); sv[7] = row_bcast<15>(s.scl);
+        }
+  #pragma unroll
+        for (int dtw = 0; dtw < DTW; ++dtw) {
+          const uint32_t lo = h ? s.code[dtw].z : s.code[dtw].x;
+          const uint32_t hi = h ? s.code[dtw].w : s.code[dtw].y;
+          const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+          const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+          const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+          const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+          const bf16x8 vop = __builtin_bit_cast(
+              bf16x8, make_uint4(pack_bf16x2(f01.x * sv[0], f01.y * sv[1]), pack_bf16x2(f23.x * sv[2], f23.y * sv[3]),
+                                 pack_bf16x2(f45.x * sv[4], f45.y * sv[5]), pack_bf16x2(f67.x * sv[6], f67.y * sv[7])));
+  #pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            acc[dtw][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dtw][nt], 0, 0, 0);
+        }
+      }
+    };
+    for (int st0 = 0; st0 < nstage; st0 += SD) {
+  #pragma unroll
+      for (int i = 0; i < SD; ++i) {
+        if (st0 + i >= nstage) break;
+        compute_v(st0 + i, ring[i]);
+        load_v(st0 + i + SD, ring[i]);
+      }
+    }
+
+    // lane (g, n) holds rows nt*16+n, dims tg*DTW*16 + dtw*16 + 4g .. +3; parts summed in order
+    if (TP > 1) {
+  #pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = nt * 16 + n;
+        if (row < a.R && pt > 0) {
+  #pragma unroll
+          for (int dtw = 0; dtw < DTW; ++dtw)
+            *reinterpret_cast<f32x4*>(lparts + ((pt * a.R + row) * D + tg * DTW * 16 + dtw * 16 + 4 * g)) = acc[dtw][nt];
+        }
+      }
+      __syncthreads();
+    }
+    if (pt == 0) {
+  #pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int row = nt * 16 + n;
+        if (row < a.R) {
+  #pragma unroll
+          for (int dtw = 0; dtw < DTW; ++dtw) {
+            const int d0 = tg * DTW * 16 + dtw * 16 + 4 * g;
+            f32x4 v = acc[dtw][nt];
+            for (int p2 = 1; p2 < TP; ++p2) v += *reinterpret_cast<const f32x4*>(lparts + ((p2 * a.R + row) * D + d0));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs,
+                                                   (int)((item * pstride + (int64_t)row * D + d0) * 4), 0, 16);
+          }
+        }
+      }
+    }
+  }
+
+  // ------------------------------------------------------------------ 3. ticket, output
+  SDV_VMCNT0();
+  __syncthreads();
+  // every workgroup of the group waits for all partials, then sums its slice of the outputs
+  // (item c of nvq slices) over the items in order -- no single workgroup reads them all
+  unsigned* ticket = sync_ticket(a, grp);
+  if (tid == 0) {
+    __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned spins = 0;
+    while (__hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)nvq) {
+      if (++spins > (1u << 20)) {
+        __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+  const int n4 = a.R * D / 4;
+  const int per = (n4 + nvq - 1) / nvq;
+  const int lo = c * per, hi = min(n4, lo + per);
+  for (int o4 = lo + tid; o4 < hi; o4 += NTHR) {
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int cc = 0;
+    for (; cc + 8 <= nvq; cc += 8) {
+      u32x4_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(((item0 + cc + u) * pstride + 4 * o4) * 4), 0, 16);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float4 f = __builtin_bit_cast(float4, v[u]);
+        s.x += f.x; s.y += f.y; s.z += f.z; s.w += f.w;
+      }
+    }
+    for (; cc < nvq; ++cc) {
+      const float4 f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(((item0 + cc) * pstride + 4 * o4) * 4), 0, 16));
+      s.x += f.x; s.y += f.y; s.z += f.z; s.w += f.w;
+    }
+    const int row = (4 * o4) / D, d = 4 * o4 - row * D, hl = row / a.S, si = row % a.S;
+    uint16_t* dst = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
+  }
+  // the last workgroup past the wait zeroes the group's statistics and counters for the next call
+  if (tid == 0) s_last = __hip_atomic_fetch_add(ticket + 16, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)nvq - 1;
+  __syncthreads();
+  if (!s_last) return;
+  for (int e = tid; e < nvq * a.R; e += NTHR) store_dev_f2(fs + (int64_t)(item0 + e / a.R) * 64 + e % a.R, make_float2(0.0f, 0.0f));
+  if (tid == 0) {
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ticket + 16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ void zero_kernel(uint32_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
 // ---------------------------------------------------------------------------- planning
 struct Plan {
   int NT, n_row_groups, rpad;
   int qk_bpw, qk_chunk_tokens, n_qk_chunks;
   int pv_bpw, pv_chunk_tokens, n_pv_chunks;
   int score_stride;
-  size_t off_stats, off_partial, total;
+  size_t off_scores, off_stats, off_partial;     // three-launch layout (after the sync area)
+  int64_t groups;
+  size_t off_fpart, fpart_bytes;                 // fused layout (statistics live in the sync area)
+  size_t total;                                   // bytes for either layout
 };
 
 static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len, Plan* p) {
@@ -546,13 +1167,125 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->n_pv_chunks = (max_seq_len + p->pv_chunk_tokens - 1) / p->pv_chunk_tokens;
   p->score_stride = max(p->n_qk_chunks * p->qk_chunk_tokens, p->n_pv_chunks * p->pv_chunk_tokens);
   const int64_t groups = (int64_t)L * B * KV;
+  p->groups = groups;
+  // the sync area [0, kSyncBytes) is shared by both layouts and only the fused kernel uses it
   const size_t scores = round_up((size_t)(groups * R * p->score_stride * 2), 256);
   const size_t stats = round_up((size_t)(groups * p->n_qk_chunks * p->rpad * 8), 256);
   const size_t partial = round_up((size_t)(groups * p->n_pv_chunks * R * D * 4), 256);
-  p->off_stats = scores;
-  p->off_partial = scores + stats;
-  p->total = scores + stats + partial;
+  p->off_scores = kSyncBytes;
+  p->off_stats = p->off_scores + scores;
+  p->off_partial = p->off_stats + stats;
+  const size_t three = p->off_partial + partial;
+  // fused: per-item fp32 partials for at most kFusedMaxItems items, 64 per group, >= 1 block each
+  const int64_t gblocks = (max_seq_len + kBlock - 1) / kBlock;
+  const int64_t per_group = gblocks < kFusedMaxChunks ? gblocks : kFusedMaxChunks;
+  const int64_t fitems = groups * per_group < kFusedMaxItems ? groups * per_group : kFusedMaxItems;
+  p->fpart_bytes = round_up((size_t)(fitems * R * D * 4), 256);
+  p->off_fpart = kSyncBytes;
+  const size_t fused = p->off_fpart + p->fpart_bytes;
+  p->total = three > fused ? three : fused;
   return true;
+}
+
+// Resident workgroup capacity of fused_kernel<D, NT> with `lds` bytes of dynamic LDS on the
+// current device (cached per device and 4 KiB LDS bucket); 0 when the device cannot run it.
+// Above 64 KiB of dynamic LDS the kernel's limit is raised first (once per device and size).
+template <int D, int NT>
+static int fused_capacity(size_t lds) {
+  constexpr int kBuckets = 41;  // 0 .. 160 KiB
+  static std::atomic<int> cache[64][kBuckets];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  const int bucket = (int)((lds + 4095) / 4096);
+  if (bucket >= kBuckets) return 0;
+  int cap = cache[dev][bucket].load(std::memory_order_relaxed);
+  if (cap > 0) return cap;
+  if ((size_t)bucket * 4096 > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fused_kernel<D, NT>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bucket * 4096) != hipSuccess) {
+    (void)hipGetLastError();  // leave no error behind for the launch status check
+    return 0;
+  }
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, NT>, 64 * fused_waves<NT>(),
+                                                   (size_t)bucket * 4096) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  cap = per_cu * cus;
+  cache[dev][bucket].store(cap, std::memory_order_relaxed);
+  return cap;
+}
+
+struct FusedShape {
+  int gb, base, extra, maxblk, grid;
+  size_t lds;
+};
+
+// The single-launch shape: as many workgroups as the device holds at once (at most 64 items
+// per group, items of at least one page block), or false when the three-launch path must
+// serve the call (several query-row groups, too many groups, items too large for LDS).
+template <int D, int NT>
+static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
+#ifdef SDV_TUNE_NO_FUSED  // tuning builds only: always the three-launch path
+  return false;
+#endif
+  constexpr int W = fused_waves<NT>();
+  if (p.n_row_groups != 1 || p.groups > kFusedMaxGroups) return false;
+  const int G = (int)p.groups;
+  const int gb = (max_seq_len + kBlock - 1) / kBlock;
+  const int max_items = min(kFusedMaxChunks, gb);
+  int cap = fused_capacity<D, NT>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total);
+  for (int iter = 0; iter < 4; ++iter) {
+    if (cap < G) return false;
+    const int base = min(max_items, cap / G);
+    const int maxblk = (gb + base - 1) / base;
+    const size_t lds = (size_t)fused_lds_layout(R, D, maxblk, W, NT == 1).total;
+    if (lds > 160 * 1024) return false;
+    const int cap2 = fused_capacity<D, NT>(lds);
+    if (cap2 < cap) {  // a wider item needs more LDS: the device holds fewer of them
+      cap = cap2;
+      continue;
+    }
+    const int extra = base < max_items ? min(G - 1, cap - G * base) : 0;
+    const int grid = G * base + extra;
+    if (grid > kFusedMaxItems || (size_t)grid * R * D * 4 > p.fpart_bytes) return false;
+    f->gb = gb;
+    f->base = base;
+    f->extra = extra;
+    f->maxblk = maxblk;  // groups with base+1 items have smaller items
+    f->grid = grid;
+    f->lds = lds;
+    return true;
+  }
+  return false;
+}
+
+template <int D, int NT>
+static bool try_fused(AttnArgs a, const Plan& p, hipStream_t st) {
+  FusedShape f;
+  if (!fused_shape<D, NT>(p, a.R, a.max_seq_len, &f)) return false;
+  a.f_gb = f.gb;
+  a.f_base = f.base;
+  a.f_extra = f.extra;
+  a.f_maxblk = f.maxblk;
+  hipLaunchKernelGGL((fused_kernel<D, NT>), dim3((unsigned)f.grid), dim3(64 * fused_waves<NT>()), f.lds, st, a);
+  return true;
+}
+
+// workgroups of the single-launch kernel for these sizes, or 0 (three-launch path)
+template <int D>
+static int fused_grid_for(const Plan& p, int R, int max_seq_len) {
+  FusedShape f;
+  bool ok = false;
+  switch (p.NT) {
+    case 1: ok = fused_shape<D, 1>(p, R, max_seq_len, &f); break;
+    case 2: ok = fused_shape<D, 2>(p, R, max_seq_len, &f); break;
+    case 3: ok = fused_shape<D, 3>(p, R, max_seq_len, &f); break;
+    default: ok = fused_shape<D, 4>(p, R, max_seq_len, &f); break;
+  }
+  return ok ? f.grid : 0;
 }
 
 template <int D, int NT>
@@ -566,6 +1299,16 @@ static void launch_qk_pv(const AttnArgs& a, const Plan& p, int zdim, hipStream_t
 
 template <int D>
 static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
+  if (phases == SDV_PHASE_ALL) {
+    bool done = false;
+    switch (p.NT) {
+      case 1: done = try_fused<D, 1>(a, p, st); break;
+      case 2: done = try_fused<D, 2>(a, p, st); break;
+      case 3: done = try_fused<D, 3>(a, p, st); break;
+      default: done = try_fused<D, 4>(a, p, st); break;
+    }
+    if (done) return;
+  }
   switch (p.NT) {
     case 1: launch_qk_pv<D, 1>(a, p, zdim, st, phases); break;
     case 2: launch_qk_pv<D, 2>(a, p, zdim, st, phases); break;
@@ -628,9 +1371,13 @@ extern "C" int sdv_paged_attention_phases(const void* q, const void* k_pages, co
   a.seq_lens = seq_lens;
   a.out = static_cast<uint16_t*>(out);
   char* ws = static_cast<char*>(workspace);
-  a.scores = reinterpret_cast<uint16_t*>(ws);
+  a.scores = reinterpret_cast<uint16_t*>(ws + p.off_scores);
   a.stats = reinterpret_cast<float2*>(ws + p.off_stats);
   a.partial = reinterpret_cast<float*>(ws + p.off_partial);
+  a.sync = reinterpret_cast<unsigned*>(ws);
+  a.fpart = reinterpret_cast<float*>(ws + p.off_fpart);
+  a.fpart_bytes = (int64_t)p.fpart_bytes;
+  a.f_gb = a.f_base = a.f_extra = a.f_maxblk = 0;  // chosen at launch
   const int64_t D = head_dim, S = q_len, H = q_heads;
   a.q_sb = H * S * D;
   a.q_ls = (int64_t)batch * a.q_sb;
@@ -682,4 +1429,21 @@ extern "C" int sdv_paged_attention(const void* q, const void* k_pages, const voi
                                     s_layer_stride, block_table, max_blocks_per_seq, seq_lens, num_layers, batch,
                                     q_heads, kv_heads, q_len, head_dim, max_seq_len, q_token_major, workspace,
                                     workspace_bytes, out, stream, SDV_PHASE_ALL);
+}
+
+extern "C" int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return SDV_ERR_NULL;
+  if (!aligned(workspace, 256) || workspace_bytes < kSyncBytes) return SDV_ERR_WORKSPACE;
+  hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint32_t*>(workspace), kSyncBytes / 4);
+  return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
+}
+
+extern "C" int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                                              int32_t q_len, int32_t head_dim, int32_t max_seq_len) {
+  if (head_dim != 64 && head_dim != 128) return 0;
+  Plan p;
+  if (!make_plan(num_layers, batch, q_heads, kv_heads, q_len, head_dim, max_seq_len, &p)) return 0;
+  const int R = (q_heads / kv_heads) * q_len;
+  return head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len) : fused_grid_for<64>(p, R, max_seq_len);
 }

@@ -19,6 +19,7 @@ Operators
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -30,6 +31,7 @@ _SCALE_MODES = {"div": _native.SCALE_DIV, "rcp": _native.SCALE_RCP}
 _BACKENDS = ("hip", "cuda")  # "cuda" is what reference call sites pass (patch.py:107)
 
 _WORKSPACES: dict = {}
+_READY: dict = {}  # id(tensor) -> weakref of workspaces whose sync prefix is known to be zero
 
 
 def _fail(msg: str):
@@ -75,15 +77,44 @@ def _pages_dims(k_pages, v_pages, v_scales, layered: bool):
     return nb, kv, d
 
 
+def new_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A fresh uint8 workspace of at least nbytes whose synchronisation prefix is zeroed
+    (sdv_attention_workspace_init on the current stream)."""
+    dev = torch.device(device)
+    ws = torch.empty(max(int(nbytes), _native.SYNC_BYTES), dtype=torch.uint8, device=dev)
+    _init_workspace(ws)
+    return ws
+
+
+def _init_workspace(ws: torch.Tensor) -> None:
+    _native.check(_native.load().sdv_attention_workspace_init(_p(ws), ws.numel(), _stream(ws.device)),
+                  "sdv_attention_workspace_init")
+    key = id(ws)
+    _READY[key] = weakref.ref(ws, lambda _r, key=key: _READY.pop(key, None))
+
+
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A cached uint8 workspace of at least nbytes on (device, current stream)."""
     dev = torch.device(device)
     key = (dev, torch.cuda.current_stream(dev).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        ws = new_workspace(dev, max(nbytes, 1 << 20))
         _WORKSPACES[key] = ws
     return ws
+
+
+def single_launch_workgroups(num_layers: int, batch: int, q_heads: int, kv_heads: int, q_len: int, head_dim: int,
+                             max_seq_len: int) -> int:
+    """Workgroups of the single-launch kernel for these sizes on the current device, or 0
+    when paged_attention takes the three-launch path."""
+    return int(_native.load().sdv_attention_single_launch(num_layers, batch, q_heads, kv_heads, q_len, head_dim,
+                                                           max_seq_len))
+
+
+def sync_errors(ws: torch.Tensor) -> int:
+    """Expired waits of the single-launch path recorded in a workspace (synchronises)."""
+    return int(ws[:4].view(torch.int32).item())
 
 
 def attention_workspace_bytes(num_layers: int, batch: int, q_heads: int, kv_heads: int, q_len: int,
@@ -182,6 +213,13 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
     nbytes = attention_workspace_bytes(L, B, H, kv, S, d, max_seq_len)
     if workspace_tensor is None:
         workspace_tensor = workspace(dev, nbytes)
+    else:
+        _need(workspace_tensor, "workspace_tensor", (torch.uint8,), dev)
+        if workspace_tensor.numel() < nbytes:
+            _fail(f"workspace_tensor holds {workspace_tensor.numel()} bytes, {nbytes} needed")
+        ref = _READY.get(id(workspace_tensor))
+        if ref is None or ref() is not workspace_tensor:  # a caller's own buffer: zero its sync prefix once
+            _init_workspace(workspace_tensor)
     per = lambda t: t[0].numel() if layered else 0  # noqa: E731
     args = (_p(q), _p(k_pages), _p(v_pages), _p(v_scales), nb, per(k_pages), per(v_pages), per(v_scales),
             _p(block_table), block_table.shape[1], _p(seq_lens), L, B, H, kv, S, d, max_seq_len,

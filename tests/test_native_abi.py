@@ -20,7 +20,7 @@ def lib():
 
 def _declared():
     text = (ROOT / "include" / "sdv.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(sdv_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int32_t|size_t|const char\*)\s+(sdv_\w+)\s*\(", text, re.M)))
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -93,6 +93,16 @@ def test_workspace_size_is_pure_host(lib):
     assert a % 256 == 0
     assert lib.sdv_attention_workspace_size(1, 1, 12, 2, 1, 96, 8192) == 0
     assert lib.sdv_attention_workspace_size(1, 1, 12, 5, 1, 128, 8192) == 0
+
+
+def test_workspace_init_validation(lib):
+    assert lib.sdv_attention_workspace_init(N, 1 << 21, N) == _native.SDV_ERR_NULL
+    assert lib.sdv_attention_workspace_init(P, _native.SYNC_BYTES - 4, N) == _native.SDV_ERR_WORKSPACE
+    assert lib.sdv_attention_workspace_init(ctypes.c_void_p(0x1010), 1 << 21, N) == _native.SDV_ERR_WORKSPACE
+    # every attention workspace holds the synchronisation prefix
+    assert lib.sdv_attention_workspace_size(1, 1, 12, 2, 1, 128, 16) >= _native.SYNC_BYTES
+    header = (ROOT / "include" / "sdv.h").read_text()
+    assert f"#define SDV_SYNC_BYTES {_native.SYNC_BYTES}" in header
 
 
 def test_encode_validation(lib):

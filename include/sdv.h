@@ -93,7 +93,7 @@ size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q
  * single-launch path that expired (0 unless its workgroups could not all be resident).
  * No counterpart in the reference (it has no workspace).
  */
-#define SDV_SYNC_BYTES 2621696
+#define SDV_SYNC_BYTES 10486016
 int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /*

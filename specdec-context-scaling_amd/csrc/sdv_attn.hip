@@ -49,9 +49,7 @@ struct AttnArgs {
   uint16_t* scores;
   float2* stats;
   float* partial;
-  unsigned* sync;   // fused path: expired-wait count, tickets, published statistics (zero between calls)
-  float* fpart;     // fused path: per-item fp32 partial outputs
-  int64_t fpart_bytes;
+  unsigned* sync;   // fused path: expired-wait count, published statistics and partials (zero between calls)
   int f_gb, f_base, f_extra, f_maxblk;  // fused: blocks per group, items per group (+1 for the first f_extra groups), LDS width
   int64_t q_ls, q_sb, q_sh, q_ss;  // element strides of q/out: layer, batch, head, row
   int max_blocks, num_blocks, max_seq_len;
@@ -534,26 +532,29 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
 //      depend on which wavefront took which block -- published to device memory.  A
 //      published entry is never all-zero bits (sum >= 1, or max = -inf), so zero means "not
 //      yet": no counter is needed for this step.
-//   2. Once every non-empty item of the group has published, the group's statistics are
-//      merged in a fixed order; each wavefront runs p.V for one 16-dimension tile (or more)
-//      and one part of the item's blocks; parts are summed in LDS in order and the fp32
-//      partial is published.
-//   3. Every workgroup of the group takes a ticket, waits until all partials are published,
-//      and sums its slice of the outputs over the items in order (the result does not
-//      depend on the order workgroups finish) into the BF16 output; the last one past the
-//      wait zeroes the group's entries and counters for the next call.
+//   2. Once every non-empty item of the group has published (one wavefront polls, the
+//      others keep their first V loads in flight), the group's statistics are merged in a
+//      fixed order; the wavefronts run p.V over the item's blocks; per-unit results are
+//      summed in LDS in order and the fp32 partial is published.
+//   3. Workgroup c of the group owns a slice of the outputs: it polls the slice of every
+//      item's partial (a published partial word is its bits + 1, so zero means "not yet"),
+//      sums it over the items in order (the result does not depend on the order workgroups
+//      finish) into the BF16 output, and clears what it read plus a share of the
+//      statistics for the next call.
 // Cross-workgroup data moves through device-scope (sc1) stores and loads, which bypass the
-// per-XCD L2 caches; `s_waitcnt vmcnt(0)` before the ticket orders the partial ahead of it.
-// No cache-writeback fence is issued (on gfx950 each agent-scope release costs ~40 ns and
-// serialises chip-wide).  Deadlock freedom: a workgroup publishes before it waits and the
-// grid never exceeds the device's resident capacity (occupancy query), so every entry a
-// wait needs comes from a running workgroup.  Waits are bounded; on expiry they count an
-// error in word 0 of the synchronisation area and continue.
-constexpr int kFusedMaxGroups = 4096;   // tickets in the synchronisation area
+// per-XCD L2 caches; every published word carries its own "written" mark, so no counter,
+// ticket or cache-writeback fence is needed (on gfx950 each agent-scope release costs
+// ~40 ns and serialises chip-wide; a counter round trip costs ~1.3 us across XCDs).
+// Deadlock freedom: a workgroup publishes before it waits and the grid never exceeds the
+// device's resident capacity (occupancy query), so every entry a wait needs comes from a
+// running workgroup.  Waits are bounded; on expiry they count an error in word 0 of the
+// synchronisation area and continue.
 constexpr int kFusedMaxItems = 4096;    // published (max, sum) rows: 64 per item
 constexpr int kFusedMaxChunks = 64;     // items per group
-constexpr size_t kSyncTicketWords = 64 + (size_t)kFusedMaxGroups * 32;  // tickets 128 bytes apart
-constexpr size_t kSyncBytes = kSyncTicketWords * 4 + (size_t)kFusedMaxItems * 64 * 8;
+constexpr size_t kSyncHeadBytes = 256;  // word 0: expired waits
+constexpr size_t kSyncStatsBytes = (size_t)kFusedMaxItems * 64 * 8;
+constexpr size_t kSyncPartBytes = (size_t)8 << 20;  // fp32 partials of one call's items
+constexpr size_t kSyncBytes = kSyncHeadBytes + kSyncStatsBytes + kSyncPartBytes;
 static_assert(kSyncBytes == SDV_SYNC_BYTES, "sdv.h states the synchronisation prefix size");
 
 #define SDV_VMCNT0() __builtin_amdgcn_s_waitcnt(0x0F70)  // vmcnt(0); exp/lgkm counters untouched
@@ -566,9 +567,24 @@ __device__ __forceinline__ uint64_t load_dev_u64(const float2* p) {
   return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float2* sync_stats(const AttnArgs& a) {
-  return reinterpret_cast<float2*>(a.sync + kSyncTicketWords);
+  return reinterpret_cast<float2*>(reinterpret_cast<char*>(a.sync) + kSyncHeadBytes);
 }
-__device__ __forceinline__ unsigned* sync_ticket(const AttnArgs& a, int grp) { return a.sync + 64 + grp * 32; }
+__device__ __forceinline__ float* sync_parts(const AttnArgs& a) {
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(a.sync) + kSyncHeadBytes + kSyncStatsBytes);
+}
+// A published partial word holds the float's bits + 1, so 0 always means "not yet written"
+// (the one pattern that would wrap, NaN 0xFFFFFFFF, is stored as a quiet NaN).
+__device__ __forceinline__ uint32_t part_word(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return u == 0xFFFFFFFFu ? 0x7FC00001u : u + 1u;
+}
+__device__ __forceinline__ u32x4_t part_enc(f32x4 v) {
+  return (u32x4_t){part_word(v[0]), part_word(v[1]), part_word(v[2]), part_word(v[3])};
+}
+__device__ __forceinline__ float4 part_dec(u32x4_t w) {
+  return make_float4(__builtin_bit_cast(float, w[0] - 1u), __builtin_bit_cast(float, w[1] - 1u),
+                     __builtin_bit_cast(float, w[2] - 1u), __builtin_bit_cast(float, w[3] - 1u));
+}
 
 // wavefronts of the fused workgroup for NT row tiles
 template <int NT>
@@ -579,7 +595,7 @@ constexpr int kVStages = 6;  // p.V stages in flight per wavefront
 // one row tile the p.V work is claimed in units and each unit's result gets an LDS slot
 // ([stage][R][D] floats); otherwise the parts of the static split ([parts][R][D]).
 struct FusedLds {
-  int scores, bstats, pages, parts, total;
+  int scores, bstats, pages, gstats, parts, red, total;
 };
 __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool claim_pv) {
   const int DT = D / 16, ntg = DT < W ? DT : W, tp = W / ntg;
@@ -587,8 +603,12 @@ __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, i
   l.scores = 0;                                                            // [R][16*maxblk + 8] bf16
   l.bstats = (l.scores + R * (maxblk * kBlock + 8) * 2 + 15) & ~15;        // [maxblk][R] float2
   l.pages = l.bstats + maxblk * R * 8;                                     // [maxblk] int
-  l.parts = (l.pages + maxblk * 4 + 15) & ~15;
+  l.gstats = (l.pages + maxblk * 4 + 15) & ~15;                           // [64] float2
+  l.parts = l.gstats + 64 * 8;
   l.total = l.parts + (claim_pv ? (maxblk + 3) / 4 : (tp > 1 ? tp : 0)) * R * D * 4;
+  l.red = 0;  // output stage, after p.V: one 16-byte chunk per (item, owned chunk)
+  const int red_bytes = (R * D / 4 + kFusedMaxChunks) * 16;
+  if (l.total < red_bytes) l.total = red_bytes;
   return l;
 }
 
@@ -599,10 +619,13 @@ __global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs 
   constexpr int NTG = DT < W ? DT : W;   // dimension-tile groups in p.V
   constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
   constexpr int TP = W / NTG;            // block parts in p.V
-  constexpr int P = 2;                   // page blocks per q.k^T claim
+#ifndef SDV_TUNE_QK_CLAIM
+#define SDV_TUNE_QK_CLAIM 1
+#endif
+  constexpr int P = SDV_TUNE_QK_CLAIM;   // page blocks per q.k^T claim
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   extern __shared__ uint4 smem_u4[];
-  __shared__ int s_next, s_next2, s_last;
+  __shared__ int s_next, s_next2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int item = blockIdx.x;
   const int big = a.f_extra * (a.f_base + 1);  // workgroups of the groups with one more item
@@ -755,51 +778,63 @@ __global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs 
   // ------------------------------------------------------------------ 2. p.V
   const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
   const float* slayer = a.v_scales + layer * a.s_ls;
-  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(a.fpart, (short)0, (int)a.fpart_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(sync_parts(a), (short)0, (int)kSyncPartBytes, 0x00020000);
   const int64_t pstride = (int64_t)a.R * D;  // floats per item
   float* lparts = reinterpret_cast<float*>(smem + lay.parts);
-  // the group's statistics: wait until all nvq items have published (each wavefront on its
-  // own), then merge in a fixed order -- lane group g takes items g, g+4, ..., then the xor
-  // tree -- so every lane, wavefront and workgroup of the group gets identical values
+  float2* lgs = reinterpret_cast<float2*>(smem + lay.gstats);  // per row: group (max, 1/sum)
+  // the group's statistics: wavefront 0 waits until all nvq items have published, merges them
+  // in a fixed order -- lane group g takes items g, g+4, ..., then the xor tree -- and shares
+  // (max, 1/sum) of each row through LDS, so every wavefront and workgroup of the group gets
+  // identical values.  The other wavefronts' V loads stay in flight across the barrier.
   auto group_stats = [&](float (&gm)[NT], float (&ginv)[NT]) {
-    const int ne = (nvq - g + 3) >> 2;  // items of this lane group
-    const int ne_max = (nvq + 3) >> 2;  // wave-uniform loop bound
+    if (wave == 0) {
+      constexpr int PB = D == 128 ? 16 : 8;  // entries in flight per lane (registers allow)
+      const int ne = (nvq - g + 3) >> 2;     // items of this lane group (<= 16)
+      const int ne_max = (nvq + 3) >> 2;  // wave-uniform loop bound
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int rr = nt * 16 + n;
+        const float2* fp = fs + (int64_t)item0 * 64 + (rr < a.R ? rr : 0);
+        float m = -INFINITY, l = 0.0f;
+        for (int k0 = 0; k0 < ne_max; k0 += PB) {
+          uint64_t e[PB];
+#pragma unroll
+          for (int k = 0; k < PB; ++k) e[k] = k0 + k < ne ? load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64) : 1;
+          unsigned spins = 0;
+          for (;;) {
+            bool ready = true;
+#pragma unroll
+            for (int k = 0; k < PB; ++k) ready = ready && e[k] != 0;
+            if (__ballot(!ready) == 0) break;
+            if (++spins > (1u << 20)) {
+              if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < PB; ++k)
+              if (e[k] == 0) e[k] = load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64);
+          }
+#pragma unroll
+          for (int k = 0; k < PB; ++k) {
+            if (k0 + k < ne) {
+              const float2 v = __builtin_bit_cast(float2, e[k]);
+              merge_fast(m, l, v.x, v.y);
+            }
+          }
+        }
+        merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
+        merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+        if (g == 0 && rr < a.R) lgs[rr] = make_float2(m, 1.0f / l);
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int rr = nt * 16 + n;
-      const float2* fp = fs + (int64_t)item0 * 64 + (rr < a.R ? rr : 0);
-      float m = -INFINITY, l = 0.0f;
-      for (int k0 = 0; k0 < ne_max; k0 += 8) {
-        uint64_t e[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) e[k] = k0 + k < ne ? load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64) : 1;
-        unsigned spins = 0;
-        for (;;) {
-          bool ready = true;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) ready = ready && e[k] != 0;
-          if (__ballot(!ready) == 0) break;
-          if (++spins > (1u << 20)) {
-            if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            if (e[k] == 0) e[k] = load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (k0 + k < ne) {
-            const float2 v = __builtin_bit_cast(float2, e[k]);
-            merge_fast(m, l, v.x, v.y);
-          }
-        }
-      }
-      merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
-      merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
-      gm[nt] = m;
-      ginv[nt] = 1.0f / l;
+      const float2 v = lgs[rr < a.R ? rr : 0];
+      gm[nt] = v.x;
+      ginv[nt] = v.y;
     }
   };
 
@@ -919,7 +954,7 @@ __global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs 
     for (int o4 = tid; o4 * 4 < a.R * D; o4 += NTHR) {
       f32x4 v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
       for (int k = 0; k < nstage; ++k) v += *reinterpret_cast<const f32x4*>(lparts + k * a.R * D + 4 * o4);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
+      __builtin_amdgcn_raw_buffer_store_b128(part_enc(v), prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
     }
   } else {
     // wavefront (tile group tg, part pt): dims [tg*DTW*16, +DTW*16), blocks [pbeg, pend)
@@ -1040,8 +1075,10 @@ __global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs 
             *reinterpret_cast<f32x4*>(lparts + ((pt * a.R + row) * D + tg * DTW * 16 + dtw * 16 + 4 * g)) = acc[dtw][nt];
         }
       }
-      __syncthreads();
     }
+    // every wavefront is past its statistics before any partial is published (an owner that
+    // has seen all partials clears the statistics)
+    __syncthreads();
     if (pt == 0) {
   #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
@@ -1052,67 +1089,70 @@ __global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs 
             const int d0 = tg * DTW * 16 + dtw * 16 + 4 * g;
             f32x4 v = acc[dtw][nt];
             for (int p2 = 1; p2 < TP; ++p2) v += *reinterpret_cast<const f32x4*>(lparts + ((p2 * a.R + row) * D + d0));
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs,
-                                                   (int)((item * pstride + (int64_t)row * D + d0) * 4), 0, 16);
+            __builtin_amdgcn_raw_buffer_store_b128(part_enc(v), prs, (int)((item * pstride + (int64_t)row * D + d0) * 4),
+                                                   0, 16);
           }
         }
       }
     }
   }
 
-  // ------------------------------------------------------------------ 3. ticket, output
-  SDV_VMCNT0();
-  __syncthreads();
-  // every workgroup of the group waits for all partials, then sums its slice of the outputs
-  // (item c of nvq slices) over the items in order -- no single workgroup reads them all
-  unsigned* ticket = sync_ticket(a, grp);
-  if (tid == 0) {
-    __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // ------------------------------------------------------------------ 3. output
+  // Workgroup c < nvq of the group owns output chunks [c*per, c*per + per) (16 bytes each) and
+  // sums them over the group's items in item order.  Partial words are never 0 once written,
+  // so the owner polls the data itself.  Having seen every item's chunks it knows that every
+  // workgroup of the group is past its statistics: it clears the chunks it consumed and its
+  // share of the statistics, leaving the synchronisation area zero for the next call.
+  const int n4 = a.R * D / 4;
+  const int per = (n4 + nvq - 1) / nvq;
+  const int lo = c * per, w = max(min(n4, lo + per) - lo, 0);
+  const int nown = (n4 + per - 1) / per;  // workgroups with a non-empty share
+  const int nld = w * nvq;                 // chunks this workgroup reads
+  float4* red = reinterpret_cast<float4*>(smem + lay.red);
+  __syncthreads();  // LDS is reused below
+  for (int e0 = 0; e0 < nld; e0 += NTHR) {  // workgroup-uniform
+    const int e = e0 + tid;
+    const bool act = e < nld;
+    const int cc = act ? e / w : 0, o = act ? e - cc * w : 0;
+    const int off = (int)(((int64_t)(item0 + cc) * pstride + 4 * (lo + o)) * 4);
+    u32x4_t v = (u32x4_t){1u, 1u, 1u, 1u};
+    if (act) v = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 16);
     unsigned spins = 0;
-    while (__hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)nvq) {
+    for (;;) {
+      const bool ready = v[0] != 0u && v[1] != 0u && v[2] != 0u && v[3] != 0u;
+      if (__ballot(!ready) == 0) break;
       if (++spins > (1u << 20)) {
-        __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(1);
+      if (!ready) v = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 16);
     }
+    if (act) red[e] = part_dec(v);
   }
   __syncthreads();
-  const int n4 = a.R * D / 4;
-  const int per = (n4 + nvq - 1) / nvq;
-  const int lo = c * per, hi = min(n4, lo + per);
-  for (int o4 = lo + tid; o4 < hi; o4 += NTHR) {
-    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    int cc = 0;
-    for (; cc + 8 <= nvq; cc += 8) {
-      u32x4_t v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        v[u] = __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(((item0 + cc + u) * pstride + 4 * o4) * 4), 0, 16);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float4 f = __builtin_bit_cast(float4, v[u]);
-        s.x += f.x; s.y += f.y; s.z += f.z; s.w += f.w;
-      }
+  for (int o = tid; o < w; o += NTHR) {
+    float4 sm = red[o];
+    for (int cc = 1; cc < nvq; ++cc) {
+      const float4 f = red[cc * w + o];
+      sm.x += f.x; sm.y += f.y; sm.z += f.z; sm.w += f.w;
     }
-    for (; cc < nvq; ++cc) {
-      const float4 f = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)(((item0 + cc) * pstride + 4 * o4) * 4), 0, 16));
-      s.x += f.x; s.y += f.y; s.z += f.z; s.w += f.w;
-    }
+    const int o4 = lo + o;
     const int row = (4 * o4) / D, d = 4 * o4 - row * D, hl = row / a.S, si = row % a.S;
     uint16_t* dst = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(s.x, s.y), pack_bf16x2(s.z, s.w));
+    *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(sm.x, sm.y), pack_bf16x2(sm.z, sm.w));
   }
-  // the last workgroup past the wait zeroes the group's statistics and counters for the next call
-  if (tid == 0) s_last = __hip_atomic_fetch_add(ticket + 16, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)nvq - 1;
-  __syncthreads();
-  if (!s_last) return;
-  for (int e = tid; e < nvq * a.R; e += NTHR) store_dev_f2(fs + (int64_t)(item0 + e / a.R) * 64 + e % a.R, make_float2(0.0f, 0.0f));
-  if (tid == 0) {
-    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(ticket + 16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int e = tid; e < nld; e += NTHR) {
+    const int cc = e / w, o = e - cc * w;
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4_t){0u, 0u, 0u, 0u}, prs,
+                                           (int)(((int64_t)(item0 + cc) * pstride + 4 * (lo + o)) * 4), 0, 16);
+  }
+  if (c < nown) {
+    for (int e = c + tid * nown; e < nvq * a.R; e += NTHR * nown)
+      store_dev_f2(fs + (int64_t)(item0 + e / a.R) * 64 + e % a.R, make_float2(0.0f, 0.0f));
   }
 }
+
 
 __global__ void zero_kernel(uint32_t* p, size_t n) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
@@ -1126,7 +1166,6 @@ struct Plan {
   int score_stride;
   size_t off_scores, off_stats, off_partial;     // three-launch layout (after the sync area)
   int64_t groups;
-  size_t off_fpart, fpart_bytes;                 // fused layout (statistics live in the sync area)
   size_t total;                                   // bytes for either layout
 };
 
@@ -1175,15 +1214,8 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->off_scores = kSyncBytes;
   p->off_stats = p->off_scores + scores;
   p->off_partial = p->off_stats + stats;
-  const size_t three = p->off_partial + partial;
-  // fused: per-item fp32 partials for at most kFusedMaxItems items, 64 per group, >= 1 block each
-  const int64_t gblocks = (max_seq_len + kBlock - 1) / kBlock;
-  const int64_t per_group = gblocks < kFusedMaxChunks ? gblocks : kFusedMaxChunks;
-  const int64_t fitems = groups * per_group < kFusedMaxItems ? groups * per_group : kFusedMaxItems;
-  p->fpart_bytes = round_up((size_t)(fitems * R * D * 4), 256);
-  p->off_fpart = kSyncBytes;
-  const size_t fused = p->off_fpart + p->fpart_bytes;
-  p->total = three > fused ? three : fused;
+  // the fused kernel keeps its statistics and partials inside the sync area
+  p->total = p->off_partial + partial;
   return true;
 }
 
@@ -1232,25 +1264,27 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
   return false;
 #endif
   constexpr int W = fused_waves<NT>();
-  if (p.n_row_groups != 1 || p.groups > kFusedMaxGroups) return false;
+  if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;
   const int G = (int)p.groups;
   const int gb = (max_seq_len + kBlock - 1) / kBlock;
   const int max_items = min(kFusedMaxChunks, gb);
-  int cap = fused_capacity<D, NT>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total);
+  // items whose fp32 partials fit the sync area
+  const int part_cap = (int)(kSyncPartBytes / ((size_t)R * D * 4));
+  int cap = min(part_cap, fused_capacity<D, NT>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total));
   for (int iter = 0; iter < 4; ++iter) {
     if (cap < G) return false;
     const int base = min(max_items, cap / G);
     const int maxblk = (gb + base - 1) / base;
     const size_t lds = (size_t)fused_lds_layout(R, D, maxblk, W, NT == 1).total;
     if (lds > 160 * 1024) return false;
-    const int cap2 = fused_capacity<D, NT>(lds);
+    const int cap2 = min(part_cap, fused_capacity<D, NT>(lds));
     if (cap2 < cap) {  // a wider item needs more LDS: the device holds fewer of them
       cap = cap2;
       continue;
     }
     const int extra = base < max_items ? min(G - 1, cap - G * base) : 0;
     const int grid = G * base + extra;
-    if (grid > kFusedMaxItems || (size_t)grid * R * D * 4 > p.fpart_bytes) return false;
+    if (grid > kFusedMaxItems || grid > part_cap) return false;
     f->gb = gb;
     f->base = base;
     f->extra = extra;
@@ -1375,8 +1409,6 @@ extern "C" int sdv_paged_attention_phases(const void* q, const void* k_pages, co
   a.stats = reinterpret_cast<float2*>(ws + p.off_stats);
   a.partial = reinterpret_cast<float*>(ws + p.off_partial);
   a.sync = reinterpret_cast<unsigned*>(ws);
-  a.fpart = reinterpret_cast<float*>(ws + p.off_fpart);
-  a.fpart_bytes = (int64_t)p.fpart_bytes;
   a.f_gb = a.f_base = a.f_extra = a.f_maxblk = 0;  // chosen at launch
   const int64_t D = head_dim, S = q_len, H = q_heads;
   a.q_sb = H * S * D;

@@ -34,7 +34,7 @@ PHASE_REDUCE = 4
 PHASE_ALL = 7
 
 BLOCK_SIZE = 16
-SYNC_BYTES = 2621696       # SDV_SYNC_BYTES: workspace prefix the single-launch path synchronises through
+SYNC_BYTES = 10486016       # SDV_SYNC_BYTES: workspace prefix the single-launch path synchronises through
 ABI_VERSION = 1
 
 # Every symbol include/sdv.h declares, with its ctypes signature.

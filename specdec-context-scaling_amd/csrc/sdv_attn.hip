@@ -551,6 +551,10 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
 // synchronisation area and continue.
 constexpr int kFusedMaxItems = 4096;    // published (max, sum) rows: 64 per item
 constexpr int kFusedMaxChunks = 64;     // items per group
+#ifndef SDV_FUSED_MIN_BLOCKS  // tuning builds: smallest item the planner aims for
+#define SDV_FUSED_MIN_BLOCKS 1
+#endif
+constexpr int kFusedMinBlocks = SDV_FUSED_MIN_BLOCKS;
 constexpr size_t kSyncHeadBytes = 256;  // word 0: expired waits
 constexpr size_t kSyncStatsBytes = (size_t)kFusedMaxItems * 64 * 8;
 constexpr size_t kSyncPartBytes = (size_t)8 << 20;  // fp32 partials of one call's items
@@ -1267,7 +1271,9 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
   if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;
   const int G = (int)p.groups;
   const int gb = (max_seq_len + kBlock - 1) / kBlock;
-  const int max_items = min(kFusedMaxChunks, gb);
+  // items of at least kFusedMinBlocks blocks: a small problem (one layer) spread over every CU
+  // would spend its time in the cross-workgroup exchanges, not in streaming
+  const int max_items = min(min(kFusedMaxChunks, gb), max(1, gb / kFusedMinBlocks));
   // items whose fp32 partials fit the sync area
   const int part_cap = (int)(kSyncPartBytes / ((size_t)R * D * 4));
   int cap = min(part_cap, fused_capacity<D, NT>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total));

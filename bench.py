@@ -43,6 +43,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph-leg", action="store_true", help="skip the per-layer HIP-graph figure")
+    ap.add_argument("--no-suite", action="store_true", help="skip the other BASELINE configurations")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (calibrates rocprof byte counters)")
     return ap.parse_args()
@@ -125,6 +126,7 @@ def main():
     _native.load()
     dev = torch.device("cuda:0")
     reps = build_replicas(torch, dev, args.replicas)
+    _progress(f"{args.replicas} cache replicas built")
     ws_multi = ops.workspace(dev, ops.attention_workspace_bytes(L, B, H, KV, S, D, T))
 
     def multi_step(r, phases=_native.PHASE_ALL):
@@ -215,7 +217,11 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    _progress("config 2 timed")
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds)
+    configs = None
+    if not args.no_suite:
+        configs = suite(torch, dev, reps, time_steps, cpu=not args.no_cpu_baseline)
 
     line = {
         "metric": "decode-attn HBM GB/s (% of ~8 TB/s peak) + us/layer at 8K ctx, FP8-V cache",
@@ -244,8 +250,202 @@ def main():
                      "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3), "traffic": traffic},
         "per_layer_graph": graph_leg,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
+
+
+def _progress(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _gbs(nbytes, us):
+    return round(nbytes / (us * 1e-6) / 1e9, 1)
+
+
+def _cpu_time(fn, budget_s):
+    """Median seconds of fn() over a bounded sample (warm-up 1, at least 3 runs)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def suite(torch, dev, reps8k, time_steps, cpu=True):
+    """The other BASELINE configurations on this GPU (and their CPU rows, briefly timed).
+
+    Decode/verify rows reuse the 8K cache replicas (a shorter context reads the first blocks
+    of the same scattered block table); the draft rows build 0.5B-shaped caches (14q/2kv,
+    D=64, 24 layers); config 4 builds B=32 ragged sequences in a fragmented pool.  Each
+    figure is us per call (GPU, graph replays over rotated inputs) and GB/s of algorithmic
+    bytes.  "per_layer" rows are the engine's call pattern (one call per layer, in a graph).
+    """
+    from specdec_amd import workloads as wl
+    from specdec_amd.engine.paged_cache import PagedKVCache
+    from specdec_amd.kernels import ops
+
+    out = {"note": "working_set_MB below ~256 MB can stay in the MI355X Infinity Cache, so such rows "
+                   "are not HBM-bound"}
+
+    def attn_rows(reps, L, H, KV, D, T, S, label, per_layer=True, steps=64):
+        _progress(label)
+        B = reps[0]["bt"].shape[0]
+        qs = [torch.randn((L, B, H, S, D), device=dev).to(torch.bfloat16) for _ in reps]
+        outs = [torch.empty_like(x) for x in qs]
+        sls = [torch.full((B,), T, dtype=torch.int32, device=dev) if isinstance(T, int) else r["sl"] for r in reps]
+        tmax = T if isinstance(T, int) else max(reps[0]["lens"])
+        ws = ops.new_workspace(dev, ops.attention_workspace_bytes(L, B, H, KV, S, D, tmax))
+        ws1 = ops.new_workspace(dev, ops.attention_workspace_bytes(1, B, H, KV, S, D, tmax))
+        lens = [T] * B if isinstance(T, int) else reps[0]["lens"]
+        nbytes = L * sum(wl.bytes_attn(t, S, H, KV, D) for t in lens)
+
+        def multi(r):
+            c = reps[r]["cache"]
+            ops.paged_attention(qs[r], c.k_pages, c.v_pages, c.v_scales, reps[r]["bt"], sls[r], tmax,
+                                out=outs[r], workspace_tensor=ws)
+
+        def layers(r):
+            c = reps[r]["cache"]
+            for layer in range(L):
+                kp, vp, vs = c.layer(layer)
+                ops.paged_attention(qs[r][layer], kp, vp, vs, reps[r]["bt"], sls[r], tmax, out=outs[r][layer],
+                                    workspace_tensor=ws1)
+
+        us = time_steps(torch, multi, steps, 8, len(reps)) * 1e3
+        row = {"layers": L, "batch": B, "q_len": S, "T": T if isinstance(T, int) else "ragged",
+               "bytes": nbytes, "working_set_MB": round(len(reps) * nbytes / 1e6, 1),
+               "us_per_call": round(us, 2), "us_per_layer": round(us / L, 3),
+               "GBps": _gbs(nbytes, us), "single_launch_workgroups":
+                   ops.single_launch_workgroups(L, B, H, KV, S, D, tmax)}
+        if per_layer:
+            usl = time_steps(torch, layers, 16, 4, len(reps)) * 1e3
+            row["per_layer_calls_us_per_layer"] = round(usl / L, 3)
+            row["per_layer_calls_GBps"] = _gbs(nbytes, usl)
+        out[label] = row
+        return row
+
+    # config 0: one layer, T=2048, decode
+    reps1 = [dict(cache=_LayerView(r["cache"], 0), bt=r["bt"], sl=r["sl"]) for r in reps8k]
+    attn_rows(reps1, 1, H, KV, D, 2048, 1, "cfg0_one_layer_T2048", per_layer=False, steps=128)
+    # config 3, target verify (S=5) at 2K/4K/8K over the 28-layer cache
+    for t in (2048, 4096, 8192):
+        attn_rows(reps8k, L, H, KV, D, t, 5, f"cfg3_verify_S5_T{t}")
+    # config 3, draft chain: 5 sequential single-token decodes, 0.5B shape (14q/2kv, D=64, 24 layers)
+    dH, dKV, dD, dL = wl.DRAFT["q_heads"], wl.DRAFT["kv_heads"], wl.DRAFT["head_dim"], wl.DRAFT["layers"]
+    dreps = _build(torch, dev, dL, dKV, dD, [8192], 6, seed0=3000)
+    for t in (2048, 4096, 8192):
+        row = attn_rows(dreps, dL, dH, dKV, dD, t, 1, f"cfg3_draft_decode_T{t}")
+        row["five_decodes_us"] = round(5 * row["per_layer_calls_us_per_layer"] * dL, 1)
+    del dreps
+    # config 4: B=32 ragged contexts U{2048..32768}, fragmented pool, 1% outlier channels x20
+    lens = wl.ragged_lengths(32, 2048, 32768, seed=41)
+    creps = _build(torch, dev, L, KV, D, lens, 1, seed0=4000, outliers=True)
+    row = attn_rows(creps, L, H, KV, D, None, 1, "cfg4_batch32_ragged", steps=8)
+    fp = creps[0]["cache"].footprint()
+    row["mean_T"] = round(sum(lens) / len(lens))
+    row["footprint"] = {"fp8v_bytes": fp["fp8v_bytes"], "bf16_bytes": fp["bf16_bytes"],
+                        "saved_frac": round(fp["saved_frac"], 4), "scale_frac_of_fp8v": round(fp["scale_frac_of_fp8v"], 4)}
+    del creps
+    torch.cuda.empty_cache()
+
+    # config 1: fused quantize + append of a 2048-token chunk into 28 layers (V only, and with K)
+    v1s, slots1, k1s, pages1 = [], None, [], []
+    for r in range(4):
+        v1, slots1, _ = wl.config1(seed=10 + r, device=dev)
+        v1s.append(v1)
+        k1s.append(torch.randn_like(v1, dtype=torch.float32).to(torch.bfloat16))
+        pc = PagedKVCache(KV, D, num_layers=L, num_blocks=2048 // 16, device=dev, growable=False)
+        pages1.append(pc)
+
+    def qa(r, with_k):
+        pc = pages1[r]
+        ops.quant_append(v1s[r], slots1, pc.k_pages, pc.v_pages, pc.v_scales, k1s[r] if with_k else None)
+
+    for with_k in (False, True):
+        _progress(f"cfg1 quant_append with_k={with_k}")
+        us = time_steps(torch, lambda r, w=with_k: qa(r, w), 64, 8, 4) * 1e3
+        nb = L * wl.bytes_quant_append(2048, KV, D, with_k)
+        out["cfg1_quant_append_2048x28" + ("_with_k" if with_k else "")] = {
+            "bytes": nb, "us_per_call": round(us, 2), "GBps": _gbs(nb, us)}
+
+    if cpu:
+        _progress("cpu rows")
+        out["cpu"] = cpu_rows(budget_s=2.0)
+    return out
+
+
+class _LayerView:
+    """One layer of a multi-layer cache, shaped as a 1-layer cache (views, no copy)."""
+
+    def __init__(self, cache, layer):
+        self.k_pages = cache.k_pages[layer:layer + 1]
+        self.v_pages = cache.v_pages[layer:layer + 1]
+        self.v_scales = cache.v_scales[layer:layer + 1]
+
+    def layer(self, i):
+        return self.k_pages[i], self.v_pages[i], self.v_scales[i]
+
+
+def _build(torch, dev, layers, kv, d, lens, nrep, seed0, outliers=False):
+    """Scattered paged caches for sequences of the given lengths (N(0,1) K/V, V quantized by the
+    library's append kernel), one layer at a time to bound memory."""
+    from specdec_amd import workloads as wl
+    from specdec_amd.engine.paged_cache import PagedKVCache
+
+    reps = []
+    B = len(lens)
+    nblocks = sum(-(-t // 16) for t in lens) + 64
+    total = sum(lens)
+    for r in range(nrep):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed0 + r)
+        cache = PagedKVCache(kv, d, num_layers=layers, batch=B, num_blocks=nblocks, device=dev,
+                             seed=seed0 + 100 + r, growable=False)
+        mult = wl.outlier_mask(layers, kv, d, 0.01, g, dev) if outliers else None
+        slots = None
+        for layer in range(layers):
+            k = torch.randn((total, kv, d), generator=g, device=dev).to(torch.bfloat16)
+            v = torch.randn((total, kv, d), generator=g, device=dev)
+            if mult is not None:
+                v = v * mult[layer]
+            slots = cache.prefill(layer, k, v.to(torch.bfloat16), lens, slots)
+        reps.append(dict(cache=cache, bt=cache.block_table(), sl=cache.seq_lens_tensor(), lens=list(lens)))
+    torch.cuda.synchronize()
+    return reps
+
+
+def cpu_rows(budget_s: float):
+    """The reference path restated in torch-CPU (oracle) for configs 0, 1 and 3 (one layer each)."""
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import attention as oatt
+    from oracle import quant as oq
+    from specdec_amd import workloads as wl
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    rows = {"cores": n, "kind": "port", "budget_s_per_row": budget_s}
+    g = wl.gen(11)
+    for label, t, s in (("cfg0_one_layer_T2048", 2048, 1), ("cfg3_verify_S5_T8192_per_layer", 8192, 5)):
+        k = wl.randn_bf16((1, KV, t - s, D), g)
+        v = wl.randn_bf16((1, KV, t - s, D), g)
+        _, cache = oatt.vfp8_decode_step(None, wl.randn_bf16((1, H, 1, D), g), k, v)
+        q = wl.randn_bf16((1, H, s, D), g)
+        kn = wl.randn_bf16((1, KV, s, D), g)
+        vn = wl.randn_bf16((1, KV, s, D), g)
+        med, nrun = _cpu_time(lambda: oatt.vfp8_decode_step(cache, q, kn, vn), budget_s)
+        nbytes = wl.bytes_attn(t, s, H, KV, D)
+        rows[label] = {"us": round(med * 1e6, 1), "GBps": round(nbytes / med / 1e9, 3), "runs": nrun}
+    v1, _, _ = wl.config1(seed=10)
+    med, nrun = _cpu_time(lambda: [oq.quantize_kv_fp8(v1[layer], D) for layer in range(L)], budget_s)
+    nb = L * wl.bytes_quant_append(2048, KV, D, False)
+    rows["cfg1_quant_2048x28"] = {"us": round(med * 1e6, 1), "GBps": round(nb / med / 1e9, 3), "runs": nrun}
+    return rows
 
 
 def cpu_baseline(budget_s: float):

@@ -163,6 +163,34 @@ class PagedKVCache:
         for b in range(B):
             self.lengths[b] = starts[b] + S
 
+    def varlen_slots(self, lengths: list[int]) -> torch.Tensor:
+        """int32 (sum(lengths),) slots of positions 0..lengths[b]-1 of each sequence in turn."""
+        out = []
+        for b, n in enumerate(lengths):
+            pos = torch.arange(n, dtype=torch.int64)
+            blk = torch.tensor(self.blocks[b][:-(-n // BLOCK)], dtype=torch.int64)
+            out.append(blk[pos // BLOCK] * BLOCK + pos % BLOCK)
+        return torch.cat(out).to(torch.int32).to(self.device)
+
+    def prefill(self, layer: int, k_new: torch.Tensor, v_new: torch.Tensor, lengths: list[int],
+                slots: torch.Tensor | None = None) -> torch.Tensor:
+        """Write whole prompts of different lengths into one layer (one kernel 1 launch).
+
+        k_new/v_new BF16 (sum(lengths), KV, D), sequence after sequence (the varlen layout);
+        lengths become ``lengths``.  Returns the slot mapping so that later layers can pass it.
+        """
+        if len(lengths) != self.batch:
+            raise ValueError(f"{len(lengths)} lengths for a batch of {self.batch}")
+        for b, n in enumerate(lengths):
+            self.reserve(b, n)
+        if slots is None:
+            slots = self.varlen_slots(lengths)
+        kp, vp, vs = self.layer(layer)
+        ops.quant_append(v_new, slots, kp, vp, vs, k_new, scale_mode=self.scale_mode)
+        for b, n in enumerate(lengths):
+            self.lengths[b] = n
+        return slots
+
     def seq_lens_tensor(self, lengths: list[int] | None = None) -> torch.Tensor:
         return torch.tensor(self.lengths if lengths is None else lengths, dtype=torch.int32).to(self.device)
 

@@ -241,3 +241,68 @@ def test_single_launch_leaves_sync_area_clean(cuda_device):
     sync = ws[:_native.SYNC_BYTES].view(torch.int32).cpu()
     assert int(sync[0]) == 0, "expired waits"
     assert int(sync.abs().sum()) == 0, "counters not reset"
+
+
+def _check_multi_layer(dev, cache, h, s, layers, seqs, label, seed):
+    """One multi-layer launch over every layer of `cache` against the eager oracle on the
+    (layer, sequence) pairs named, reading back what the append kernel wrote."""
+    from oracle import quant as oq
+    g = wl.gen(seed, dev)
+    L, B = cache.num_layers, cache.batch
+    q = torch.randn((L, B, h, s, cache.head_dim), generator=g, device=dev).to(torch.bfloat16)
+    lens = list(cache.lengths)
+    ws = ops.new_workspace(dev, ops.attention_workspace_bytes(L, B, h, cache.kv_heads, s, cache.head_dim,
+                                                              max(lens)))
+    out = ops.paged_attention(q, cache.k_pages, cache.v_pages, cache.v_scales, cache.block_table(),
+                              cache.seq_lens_tensor(), max(lens), workspace_tensor=ws)
+    torch.cuda.synchronize()
+    assert ops.sync_errors(ws) == 0, f"{label}: expired waits"
+    for layer in layers:
+        for b in seqs:
+            k, v, sc = cache.gather(layer, b)
+            v_hat = oq.dequantize_kv_fp8(v.cpu()[None], sc.cpu()[None], torch.bfloat16)
+            want = oatt.eager_attention(q[layer, b:b + 1].cpu(), k.cpu()[None], v_hat)
+            assert_close(out[layer, b:b + 1].cpu(), want, f"{label} layer {layer} seq {b} T={lens[b]}")
+
+
+def _filled_cache(dev, layers, kv, d, lens, seed, outliers=False):
+    g = wl.gen(seed, dev)
+    cache = PagedKVCache(kv, d, num_layers=layers, batch=len(lens), num_blocks=sum(-(-t // 16) for t in lens) + 9,
+                         device=dev, seed=seed, growable=False)
+    mult = wl.outlier_mask(layers, kv, d, 0.01, g, dev) if outliers else None
+    slots = None
+    for layer in range(layers):
+        k = torch.randn((sum(lens), kv, d), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((sum(lens), kv, d), generator=g, device=dev)
+        if mult is not None:
+            v = v * mult[layer]
+        slots = cache.prefill(layer, k, v.to(torch.bfloat16), lens, slots)
+    return cache
+
+
+def test_multi_layer_draft_d64(cuda_device):
+    """The 0.5B draft shape (14q/2kv, D=64) over 24 layers at 8K in one launch."""
+    announce("attn multi-layer draft 24x14/2/64 T=8192")
+    cache = _filled_cache(cuda_device, 24, 2, 64, [8192], seed=501)
+    _check_multi_layer(cuda_device, cache, 14, 1, (0, 13, 23), (0,), "draft", seed=502)
+
+
+@pytest.mark.parametrize("t", [2048, 8192])
+def test_multi_layer_verify_s5(cuda_device, t):
+    """The k+1=5-row verify over all 28 target layers in one launch."""
+    announce(f"attn multi-layer verify 28x12/2/128 S=5 T={t}")
+    cache = _filled_cache(cuda_device, 28, 2, 128, [t], seed=510 + t)
+    _check_multi_layer(cuda_device, cache, 12, 5, (0, 27), (0,), f"verify T={t}", seed=511)
+
+
+def test_multi_layer_batch32_ragged(cuda_device):
+    """Config 4: B=32 contexts U{2048..32768}, fragmented pool, 1% outlier V channels x20,
+    28 layers in one launch; the shortest, the longest and the first sequence are checked."""
+    lens = wl.ragged_lengths(32, 2048, 32768, seed=41)
+    announce(f"attn multi-layer B=32 ragged 28x12/2/128 T={min(lens)}..{max(lens)}")
+    cache = _filled_cache(cuda_device, 28, 2, 128, lens, seed=520, outliers=True)
+    seqs = sorted({0, lens.index(min(lens)), lens.index(max(lens))})
+    _check_multi_layer(cuda_device, cache, 12, 1, (0, 27), seqs, "B=32 ragged", seed=521)
+    fp = cache.footprint()
+    assert fp["tokens"] == sum(lens)
+    assert abs(fp["saved_frac"] - (1 - 776 / 1024)) < 1e-9

@@ -70,7 +70,8 @@ enum sdv_status {
  *               elements apart; k_new may be NULL: K is then not written).
  * slot_mapping: int32 [n_tokens]; a negative slot skips the token (padding).
  * group_size must equal head_dim (the v_fp8 format: one scale per token and KV head).
- * head_dim in {64, 128}.  Alignment: v_new/k_new/k_pages 4 B, v_pages 16 B, v_scales 4 B.
+ * head_dim in {64, 128}.  Alignment: v_new/k_new/k_pages/v_pages 16 B (and layer strides of
+ * v_new/k_new/k_pages multiples of 8 elements), v_scales and slot_mapping 4 B.
  * Each (token, KV head) gets s = max|v| / 448 (s == 0 -> 1), payload RNE(v / s) in E4M3FN,
  * bit-exact with the reference helper evaluated per scale_mode.
  */

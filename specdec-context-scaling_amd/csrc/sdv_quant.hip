@@ -7,12 +7,23 @@
 //
 // K is copied into the page's [D/8][16][8] chunk layout (see include/sdv.h).
 //
-// One wavefront handles 16 consecutive tokens of one KV head of one layer.  Lane l owns
-// head_dim/64 adjacent dimensions, so each token's 128-dim row is one coalesced 256-byte
-// load and the max-abs is a wave reduction (DPP row rotations + cross-row readlanes).
-// When the 16 tokens fill one page block exactly (prefill), each lane accumulates its
-// dimensions' 16 codes and writes them with one 16-byte store per dimension (the V page is
-// dimension-major); otherwise codes go out as single bytes per slot (decode append).
+// One wavefront handles 16 consecutive input tokens of one KV head of one layer; a
+// workgroup holds four such wavefronts (64 tokens).  D/8 lanes (a "row") hold one token's
+// head_dim values as 16-byte pieces, so each wave-wide load brings 64/(D/8) whole token rows
+// and a lane ends up holding J = 16 / rows consecutive tokens of the same 8 dimensions.  The
+// max-abs of a token is a DPP reduction inside its row (no cross-row traffic).  The V page
+// is dimension-major ([D][16 tokens] bytes), so when the 16 tokens fill one page block
+// exactly (prefill) each lane packs its J codes per dimension, the wave transposes them
+// through LDS, and every dimension's 16 codes leave as one 16-byte store; otherwise (decode,
+// partial or scattered blocks) codes go out as single bytes per slot.  K moves as 16-byte
+// pieces from its loads, issued with the V loads before any arithmetic, to its page chunk.
+//
+// The kernel is VALU-bound if each value takes an IEEE division and a branchy encoder, so
+// per token it forms r = RN(1/s) once, and per value takes RN(x / s) as one multiply and two
+// fma (quotient_rn) and converts with v_cvt_pk_fp8_f32 (gfx950: OCP E4M3FN, round to
+// nearest even; equal to the integer encoder for every fp32 input except the sign of a NaN,
+// which cannot occur on this route).  Tokens whose max-abs is not finite or lies in
+// (0, 2^-60) take the exact division and the integer encoder instead.
 #include "sdv_internal.h"
 
 namespace sdv {
@@ -32,96 +43,191 @@ struct QuantArgs {
   int64_t k_ls, v_ls, s_ls;
 };
 
-template <int D>
-__global__ __launch_bounds__(64) void quant_append_kernel(QuantArgs a) {
-  constexpr int DPL = D / 64;  // dimensions per lane
-  const int lane = threadIdx.x;
-  const int t0 = blockIdx.x * kBlock;
+// Max over the `LPR` lanes of each row (LPR = 8 or 16 consecutive lanes) of non-negative
+// fp32 bit patterns (unsigned compare; NaN propagates like torch.amax).  Every lane of the
+// row receives the row's maximum.
+template <int LPR>
+__device__ __forceinline__ uint32_t row_max_bits(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // half-row mirror
+  if (LPR == 16)
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+
+constexpr int kQuantWaves = 4;  // wavefronts (16-token tiles) per workgroup
+
+// Smallest max-abs (fp32 bits, 2^-60) of the fast route below: from there up to the largest
+// finite value, 1/s stays a normal fp32 and every intermediate that can change a code is normal.
+constexpr uint32_t kFastMinAmaxBits = 0x21800000u;
+
+// RN(x / s) from r = RN(1/s): q0 = RN(x r), e = x - s q0 (exact, one fma), RN(q0 + e r)
+// (Markstein's correction step).  For s = RN(max|v| / 448) or RN(max|v| * RN(1/448)) with
+// max|v| = 0 or in [2^-60, max finite], and every BF16 x with |x| <= max|v|, the E4M3FN code
+// of this value equals the code of the IEEE quotient: tests/native/quotient_check.c walks all
+// such (max|v|, x) pairs and finds no difference (fp32 results differ only below 2^-10, code 0).
+// The sign is copied from x, as the quotient by a positive s has it (also for -0).
+__device__ __forceinline__ float quotient_rn(float x, float s, float r) {
+#pragma clang fp contract(off)
+  const float ax = fabsf(x);
+  const float q0 = ax * r;
+  const float e = __builtin_fmaf(-q0, s, ax);
+  return copysignf(__builtin_fmaf(e, r, q0), x);
+}
+
+template <int D, bool WITH_K>
+__global__ __launch_bounds__(64 * kQuantWaves) void quant_append_kernel(QuantArgs a) {
+  constexpr int LPR = D / 8;          // lanes per token row: 16 bytes of BF16 each
+  constexpr int RPW = kWave / LPR;    // token rows per wave-wide load (4 or 8)
+  constexpr int J = kBlock / RPW;     // consecutive tokens held by one lane (4 or 2)
+  // per wavefront: the codes of one page block, [D][16 tokens] bytes
+  __shared__ uint4 lds_codes[kQuantWaves][D];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int r = lane / LPR, p = lane % LPR;
+  const int t0 = (blockIdx.x * kQuantWaves + wave) * kBlock;
+  if (t0 >= a.n_tokens) return;  // wave-uniform
   const int kvh = blockIdx.y;
   const int layer = blockIdx.z;
   const int nt = min(kBlock, a.n_tokens - t0);
   const int KV = a.kv_heads;
 
   const uint16_t* vin = a.v_new + layer * a.in_ls;
-  const uint16_t* kin = a.k_new ? a.k_new + layer * a.in_ls : nullptr;
+  const uint16_t* kin = a.k_new + layer * a.in_ls;
   uint16_t* kp = a.k_pages + layer * a.k_ls;
   uint8_t* vp = a.v_pages + layer * a.v_ls;
   float* sp = a.v_scales + layer * a.s_ls;
 
-  int my_slot = -1;
-  if (lane < nt) {
-    my_slot = a.slots[t0 + lane];
-    if ((int64_t)my_slot >= (int64_t)a.num_blocks * kBlock) my_slot = -1;  // out-of-range slot: skipped
-  }
-  const int slot0 = __builtin_amdgcn_readlane(my_slot, 0);
-  const uint64_t run = __ballot(lane < kBlock && my_slot == slot0 + lane);
-  const bool full = (nt == kBlock) && slot0 >= 0 && (slot0 & (kBlock - 1)) == 0 &&
-                    (run & 0xFFFFull) == 0xFFFFull;
-
-  // Issue every token's row load first (16 independent loads in flight).
-  uint32_t w[kBlock];
+  // slots first (unconditional loads from a clamped index, so that all of them are in flight
+  // together), then every V and K load: the arithmetic below waits on the slots only
+  // V: lane (r, p) holds tokens r*J .. r*J+J-1; K (no per-token arithmetic) is read with
+  // token j*RPW + r in load j, so that the lanes storing one page chunk hold consecutive tokens
+  int slot[J], kslot[J];
 #pragma unroll
-  for (int i = 0; i < kBlock; ++i) {
-    w[i] = 0;
-    if (i < nt) {
-      const uint16_t* src = vin + ((int64_t)(t0 + i) * KV + kvh) * D + DPL * lane;
-      w[i] = (DPL == 2) ? *reinterpret_cast<const uint32_t*>(src) : (uint32_t)*src;
+  for (int j = 0; j < J; ++j) {
+    slot[j] = a.slots[t0 + min(r * J + j, nt - 1)];
+    if (WITH_K) kslot[j] = a.slots[t0 + min(j * RPW + r, nt - 1)];
+  }
+  // rows past the end of the input re-read the last token (skipped below): no branches
+  // around the loads, so that none of them has to land before the slots are used
+  uint4 vw[J], kw[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    vw[j] = load_stream16(vin + ((int64_t)(t0 + min(r * J + j, nt - 1)) * KV + kvh) * D + 8 * p);
+    if (WITH_K) kw[j] = load_stream16(kin + ((int64_t)(t0 + min(j * RPW + r, nt - 1)) * KV + kvh) * D + 8 * p);
+  }
+
+  const int64_t n_slots = (int64_t)a.num_blocks * kBlock;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {  // past the end or out of range: skipped
+    if (r * J + j >= nt || (int64_t)slot[j] >= n_slots) slot[j] = -1;
+    if (WITH_K && (j * RPW + r >= nt || (int64_t)kslot[j] >= n_slots)) kslot[j] = -1;
+  }
+  const int slot0 = __builtin_amdgcn_readlane(slot[0], 0);
+  bool contiguous = true;
+#pragma unroll
+  for (int j = 0; j < J; ++j) contiguous = contiguous && slot[j] == slot0 + r * J + j;
+  const bool full = nt == kBlock && slot0 >= 0 && (slot0 & (kBlock - 1)) == 0 && __ballot(!contiguous) == 0;
+
+  // per token: scale s, its correctly rounded reciprocal, and whether the fast route holds
+  float scale[J], rcp[J];
+  bool fast[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t w[4] = {vw[j].x, vw[j].y, vw[j].z, vw[j].w};
+    uint32_t mb = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mb = max(mb, (w[i] << 16) & 0x7FFFFFFFu);
+      mb = max(mb, w[i] & 0x7FFF0000u);
+    }
+    const uint32_t ab = row_max_bits<LPR>(mb);
+    const float amax = __uint_as_float(ab);
+    float sc = (a.scale_mode == SDV_SCALE_RCP) ? amax * (1.0f / 448.0f) : amax / 448.0f;
+    if (sc == 0.0f) sc = 1.0f;
+    scale[j] = sc;
+    rcp[j] = 1.0f / sc;
+    fast[j] = ab == 0 || (ab >= kFastMinAmaxBits && ab < 0x7F800000u);
+  }
+
+  // codes: packed[k] holds dimension k's J codes, token j in byte j
+  uint32_t packed[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float q[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t wk = (k & 1) ? (&vw[j].x)[k >> 1] & 0xFFFF0000u : (&vw[j].x)[k >> 1] << 16;
+      q[j] = quotient_rn(__uint_as_float(wk), scale[j], rcp[j]);
+    }
+    uint32_t c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    if (J == 4) c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2 % J], q[3 % J], (int)c, true);
+    packed[k] = c;
+  }
+  // tokens outside the fast route (max-abs non-finite, or in (0, 2^-60)): exact division and
+  // the integer encoder, byte by byte (rare; skipped when no lane of the wave has one)
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (fast[j]) continue;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t wk = (k & 1) ? (&vw[j].x)[k >> 1] & 0xFFFF0000u : (&vw[j].x)[k >> 1] << 16;
+      const uint32_t code = e4m3fn_encode(__uint_as_float(wk) / scale[j]);
+      packed[k] = (packed[k] & ~(0xFFu << (8 * j))) | (code << (8 * j));
     }
   }
 
-  uint32_t packed[DPL][4];  // full-block path: 16 codes per owned dimension
+  if (!full) {  // decode, partial or scattered blocks: one byte per slot and dimension
 #pragma unroll
-  for (int d = 0; d < DPL; ++d)
+    for (int j = 0; j < J; ++j) {
+      if (slot[j] < 0) continue;
+      const int blk = slot[j] >> 4, off = slot[j] & (kBlock - 1);
+      uint8_t* vrow = vp + (((int64_t)blk * KV + kvh) * D + 8 * p) * kBlock + off;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) packed[d][k] = 0;
-  float my_scale = 1.0f;
-
-#pragma unroll
-  for (int i = 0; i < kBlock; ++i) {
-    const int slot = __builtin_amdgcn_readlane(my_slot, i);  // -1 beyond nt
-    if (slot < 0) continue;  // wave-uniform: padding token or past the end
-    const float x0 = bf16_lo(w[i]);
-    const float x1 = (DPL == 2) ? bf16_hi(w[i]) : 0.0f;
-    uint32_t mb = __float_as_uint(fabsf(x0));
-    if (DPL == 2) mb = max(mb, __float_as_uint(fabsf(x1)));
-    const float amax = __uint_as_float(wave_max_nonneg_bits(mb));
-    float s = (a.scale_mode == SDV_SCALE_RCP) ? amax * (1.0f / 448.0f) : amax / 448.0f;
-    if (s == 0.0f) s = 1.0f;
-    const uint32_t c0 = e4m3fn_encode(x0 / s);
-    const uint32_t c1 = (DPL == 2) ? e4m3fn_encode(x1 / s) : 0u;
-
-    const int blk = slot >> 4, off = slot & (kBlock - 1);
-    const int64_t page = (int64_t)blk * KV + kvh;
-    if (kin) {
-      // K page: [D/8 chunks][16 tokens][8 dims]; lane's dims DPL*lane.. sit in chunk DPL*lane/8
-      const uint16_t* ksrc = kin + ((int64_t)(t0 + i) * KV + kvh) * D + DPL * lane;
-      const int d0 = DPL * lane;
-      uint16_t* kdst = kp + page * kBlock * D + ((d0 >> 3) * kBlock + off) * 8 + (d0 & 7);
-      if (DPL == 2)
-        *reinterpret_cast<uint32_t*>(kdst) = *reinterpret_cast<const uint32_t*>(ksrc);
-      else
-        *kdst = *ksrc;
+      for (int k = 0; k < 8; ++k) vrow[k * kBlock] = (uint8_t)(packed[k] >> (8 * j));
+      if (p == 0) sp[((int64_t)blk * KV + kvh) * kBlock + off] = scale[j];
     }
-    if (full) {
-      packed[0][i >> 2] |= c0 << (8 * (i & 3));
-      if (DPL == 2) packed[DPL - 1][i >> 2] |= c1 << (8 * (i & 3));
-      if (lane == i) my_scale = s;
-    } else {
-      uint8_t* vrow = vp + (page * D + DPL * lane) * kBlock + off;
-      vrow[0] = (uint8_t)c0;
-      if (DPL == 2) vrow[kBlock] = (uint8_t)c1;
-      if (lane == 0) sp[page * kBlock + off] = s;
+  }
+
+  // K: 16-byte pieces into the page chunk of each token's slot
+  if (WITH_K) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if (kslot[j] < 0) continue;
+      const int blk = kslot[j] >> 4, off = kslot[j] & (kBlock - 1);
+      uint16_t* kdst = kp + ((int64_t)blk * KV + kvh) * kBlock * D + (p * kBlock + off) * 8;
+      *reinterpret_cast<uint4*>(kdst) = kw[j];
     }
   }
 
   if (full) {
-    const int64_t page = (int64_t)(slot0 >> 4) * KV + kvh;
+    // LDS transpose: lane (r, p) holds bytes [r*J, r*J+J) of dimension lines 8p..8p+7
+    uint8_t* mine = reinterpret_cast<uint8_t*>(lds_codes[wave]);
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) {
-      uint4 v4 = make_uint4(packed[d][0], packed[d][1], packed[d][2], packed[d][3]);
-      *reinterpret_cast<uint4*>(vp + (page * D + DPL * lane + d) * kBlock) = v4;
+    for (int k = 0; k < 8; ++k) {
+      uint8_t* dst = mine + (8 * p + k) * kBlock + r * J;
+      if (J == 4)
+        *reinterpret_cast<uint32_t*>(dst) = packed[k];
+      else
+        *reinterpret_cast<uint16_t*>(dst) = (uint16_t)packed[k];
     }
-    if (lane < kBlock) sp[page * kBlock + lane] = my_scale;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t page = (int64_t)(slot0 >> 4) * KV + kvh;
+    uint4* vdst = reinterpret_cast<uint4*>(vp + page * D * kBlock);
+#pragma unroll
+    for (int d = lane; d < D; d += kWave) vdst[d] = lds_codes[wave][d];
+    // scales: lane (r, p < J) writes token r*J + p (16 consecutive floats per wave)
+    if (p < J) {
+      float sc = scale[0];
+#pragma unroll
+      for (int j = 1; j < J; ++j)
+        if (p == j) sc = scale[j];
+      sp[page * kBlock + r * J + p] = sc;
+    }
   }
 }
 
@@ -150,9 +256,11 @@ extern "C" int sdv_quant_append(const void* v_new, const void* k_new, const int3
         (k_new && k_layer_stride < k_page))
       return SDV_ERR_SHAPE;
   }
-  if (!aligned(v_new, 4) || !aligned(k_new, 4) || !aligned(k_pages, 4) || !aligned(v_pages, 16) ||
+  if (!aligned(v_new, 16) || !aligned(k_new, 16) || !aligned(k_pages, 16) || !aligned(v_pages, 16) ||
       !aligned(v_scales, 4) || !aligned(slot_mapping, 4))
     return SDV_ERR_ALIGN;
+  if (num_layers > 1 && (in_layer_stride % 8 != 0 || (k_new && k_layer_stride % 8 != 0)))
+    return SDV_ERR_ALIGN;  // 16-byte rows in every layer
   if (n_tokens == 0) return SDV_OK;
 
   QuantArgs a;
@@ -171,11 +279,17 @@ extern "C" int sdv_quant_append(const void* v_new, const void* k_new, const int3
   a.v_ls = num_layers > 1 ? v_layer_stride : 0;
   a.s_ls = num_layers > 1 ? s_layer_stride : 0;
 
-  dim3 grid((n_tokens + kBlock - 1) / kBlock, kv_heads, num_layers);
+  const int tiles = (n_tokens + kBlock - 1) / kBlock;
+  dim3 grid((tiles + kQuantWaves - 1) / kQuantWaves, kv_heads, num_layers);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(quant_append_kernel<128>, grid, dim3(64), 0, st, a);
+  const dim3 block(64 * kQuantWaves);
+  if (head_dim == 128 && k_new)
+    hipLaunchKernelGGL((quant_append_kernel<128, true>), grid, block, 0, st, a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((quant_append_kernel<128, false>), grid, block, 0, st, a);
+  else if (k_new)
+    hipLaunchKernelGGL((quant_append_kernel<64, true>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL(quant_append_kernel<64>, grid, dim3(64), 0, st, a);
+    hipLaunchKernelGGL((quant_append_kernel<64, false>), grid, block, 0, st, a);
   return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
 }

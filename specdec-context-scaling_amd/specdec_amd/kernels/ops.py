@@ -159,6 +159,11 @@ def quant_append(v_new: torch.Tensor, slot_mapping: torch.Tensor, k_pages: torch
             _fail(f"k_new {tuple(k_new.shape)} != v_new {tuple(v_new.shape)}")
     if scale_mode not in _SCALE_MODES:
         raise ValueError(f"scale_mode must be one of {sorted(_SCALE_MODES)}")
+    # the kernel moves 16-byte pieces of each row; a view starting mid-row is copied first
+    if v_new.data_ptr() % 16:
+        v_new = v_new.clone()
+    if k_new is not None and k_new.data_ptr() % 16:
+        k_new = k_new.clone()
     per = lambda t: t[0].numel() if layered else 0  # noqa: E731  (elements per layer)
     st = lib.sdv_quant_append(_p(v_new), _p(k_new), _p(slot_mapping), n_tokens, kv, d, d, L,
                               per(v_new), _p(k_pages), _p(v_pages), _p(v_scales), nb,

@@ -114,14 +114,17 @@ def test_decode_appends_ragged_and_skips(cuda_device):
 def test_d64_draft_shape_multi_layer(cuda_device):
     announce("quant d64 24 layers")
     v, slots, _ = wl.config1(seed=4, tokens=512, layers=24, head_dim=64)
+    k = wl.randn_bf16(v.shape, wl.gen(5))
     kp, vp, vs = _pages(cuda_device, 24, 32, 2, 64)
-    ops.quant_append(v.to(cuda_device), slots.to(cuda_device), kp, vp, vs)
+    ops.quant_append(v.to(cuda_device), slots.to(cuda_device), kp, vp, vs, k.to(cuda_device))
     q, s = quantize_rows(v)
+    kb = bits16(k)
     for layer in (0, 11, 23):
         ek, ev, es = opaged.alloc(32, 2, 64)
-        opaged.write(None, ev, es, None, q[layer], s[layer], slots.numpy())
+        opaged.write(ek, ev, es, kb[layer], q[layer], s[layer], slots.numpy())
         assert np.array_equal(vp[layer].cpu().numpy(), ev)
         assert np.array_equal(vs[layer].cpu().numpy().view(np.uint32), es.view(np.uint32))
+        assert np.array_equal(bits16(kp[layer]), ek)
 
 
 def test_device_encoder_exhaustive(cuda_device):
@@ -140,3 +143,36 @@ def test_device_encoder_exhaustive(cuda_device):
     samp = torch.randint(-(1 << 31), (1 << 31) - 1, (1 << 20,), generator=g, dtype=torch.int64).to(torch.int32)
     ours = ops.fp8_encode(samp.view(torch.float32).to(cuda_device)).cpu().numpy()
     assert np.array_equal(ours, ofp8.encode(samp.view(torch.float32).numpy()))
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_prefill_mixed_tiles(cuda_device, d):
+    """One launch whose 16-token tiles take every path: whole aligned blocks (16-byte
+    dimension stores), a contiguous run that starts mid-block, a reversed run, a run with a
+    padding slot and an out-of-range slot, and a partial last tile; K written too."""
+    announce(f"quant mixed tiles d={d}")
+    g = wl.gen(77 + d)
+    kv, nb = 2, 16
+    slots = list(range(2 * 16, 5 * 16))                 # tiles 0-2: blocks 2, 3, 4 whole
+    slots += list(range(6 * 16 + 3, 7 * 16 + 3))        # tile 3: contiguous, not block aligned
+    slots += list(range(9 * 16 + 15, 8 * 16 - 1, -1))   # tile 4: block 8 reversed
+    t5 = list(range(10 * 16, 11 * 16))
+    t5[5], t5[11] = -1, nb * 16 + 40                     # padding and out-of-range slots: skipped
+    slots += t5
+    slots += list(range(12 * 16, 12 * 16 + 7))          # tile 6: 7 tokens of block 12
+    slots = np.array(slots, dtype=np.int32)
+    n = len(slots)
+    v = wl.randn_bf16((n, kv, d), g)
+    k = wl.randn_bf16((n, kv, d), g)
+    kp, vp, vs = _pages(cuda_device, 1, nb, kv, d)
+    ops.quant_append(v.to(cuda_device), to_dev(slots, cuda_device), kp[0], vp[0], vs[0], k.to(cuda_device))
+    torch.cuda.synchronize()
+    q, s = quantize_rows(v)
+    keep = (slots >= 0) & (slots < nb * 16)
+    ek, ev, es = opaged.alloc(nb, kv, d)
+    ev[:] = 0xA5
+    es[:] = -7.0
+    opaged.write(ek, ev, es, bits16(k)[keep], q[keep], s[keep], slots[keep])
+    assert np.array_equal(vp[0].cpu().numpy(), ev)
+    assert np.array_equal(vs[0].cpu().numpy().view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(bits16(kp[0]), ek)

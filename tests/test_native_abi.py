@@ -82,6 +82,10 @@ def test_quant_host_validation(lib):
     assert _quant(lib, n=-1) == _native.SDV_ERR_SHAPE
     assert _quant(lib, L=2, ils=5) == _native.SDV_ERR_SHAPE
     assert _quant(lib, vp=ctypes.c_void_p(0x1004)) == _native.SDV_ERR_ALIGN
+    assert _quant(lib, v=ctypes.c_void_p(0x1008)) == _native.SDV_ERR_ALIGN    # rows move as 16-byte pieces
+    assert _quant(lib, k=ctypes.c_void_p(0x1008)) == _native.SDV_ERR_ALIGN
+    assert _quant(lib, kp=ctypes.c_void_p(0x1008), k=P) == _native.SDV_ERR_ALIGN
+    assert _quant(lib, L=2, ils=16 * 2 * 128 + 4, vls=1 << 20, sls=1 << 20) == _native.SDV_ERR_ALIGN
     assert _quant(lib, n=0) == _native.SDV_OK                  # nothing to do, no launch
 
 

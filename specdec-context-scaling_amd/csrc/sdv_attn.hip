@@ -521,8 +521,8 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
 
 // ---------------------------------------------------------------------------- fused
 // One launch for the shapes whose whole grid fits the device at once (one query-row group:
-// decode and verify).  One workgroup per CU (W = 16 wavefronts for decode; 8 or 4 when the
-// row tiles need more registers), each owning one item: a run of page blocks of one
+// decode and verify).  One workgroup per CU (W = 8 or 16 wavefronts for decode; 8 or 4 when
+// the row tiles need more registers), each owning one item: a run of page blocks of one
 // (layer*batch, KV head) group.  Groups are cut into items of nearly equal size (a group
 // gets f_base or f_base+1 items), so every CU streams the same number of bytes.  Inside a
 // workgroup the wavefronts claim page blocks from an LDS counter, so a wavefront the
@@ -590,9 +590,13 @@ __device__ __forceinline__ float4 part_dec(u32x4_t w) {
                      __builtin_bit_cast(float, w[2] - 1u), __builtin_bit_cast(float, w[3] - 1u));
 }
 
-// wavefronts of the fused workgroup for NT row tiles
-template <int NT>
-constexpr int fused_waves() { return NT == 1 ? 16 : NT == 2 ? 8 : 4; }
+// wavefronts of the fused workgroup for NT row tiles.  With one row tile the workgroup is
+// alone on its CU; measured on gfx950, 8 wavefronts finish a D=128 call sooner than 16 (one
+// layer at T=2048: 12.6 us vs 13.7 us; 28 layers at 8K: equal within noise), while D=64
+// blocks are half the bytes and 16 wavefronts keep more of them in flight (24 layers at
+// 8K: 23.7 us vs 25.5 us).
+template <int D, int NT>
+constexpr int fused_waves() { return NT == 1 ? (D == 128 ? 8 : 16) : NT == 2 ? 8 : 4; }
 constexpr int kVStages = 6;  // p.V stages in flight per wavefront
 
 // dynamic LDS of a fused workgroup with items of up to `maxblk` blocks (byte offsets).  With
@@ -616,9 +620,9 @@ __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, i
   return l;
 }
 
-template <int D, int NT>
-__global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs a) {
-  constexpr int W = fused_waves<NT>(), NTHR = 64 * W;
+template <int D, int NT, int W>
+__global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
+  constexpr int NTHR = 64 * W;
   constexpr int KK = D / 32, DT = D / 16;
   constexpr int NTG = DT < W ? DT : W;   // dimension-tile groups in p.V
   constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
@@ -1135,9 +1139,21 @@ __global__ __launch_bounds__(64 * fused_waves<NT>()) void fused_kernel(AttnArgs 
     if (act) red[e] = part_dec(v);
   }
   __syncthreads();
+  // sum over the items in item order; the LDS reads go out eight at a time ahead of the
+  // adds (a plain loop is one dependent LDS round trip per item)
   for (int o = tid; o < w; o += NTHR) {
     float4 sm = red[o];
-    for (int cc = 1; cc < nvq; ++cc) {
+    int cc = 1;
+    for (; cc + 8 <= nvq; cc += 8) {
+      float4 f[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f[k] = red[(cc + k) * w + o];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        sm.x += f[k].x; sm.y += f[k].y; sm.z += f[k].z; sm.w += f[k].w;
+      }
+    }
+    for (; cc < nvq; ++cc) {
       const float4 f = red[cc * w + o];
       sm.x += f.x; sm.y += f.y; sm.z += f.z; sm.w += f.w;
     }
@@ -1226,7 +1242,7 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
 // Resident workgroup capacity of fused_kernel<D, NT> with `lds` bytes of dynamic LDS on the
 // current device (cached per device and 4 KiB LDS bucket); 0 when the device cannot run it.
 // Above 64 KiB of dynamic LDS the kernel's limit is raised first (once per device and size).
-template <int D, int NT>
+template <int D, int NT, int W>
 static int fused_capacity(size_t lds) {
   constexpr int kBuckets = 41;  // 0 .. 160 KiB
   static std::atomic<int> cache[64][kBuckets];
@@ -1237,18 +1253,21 @@ static int fused_capacity(size_t lds) {
   int cap = cache[dev][bucket].load(std::memory_order_relaxed);
   if (cap > 0) return cap;
   if ((size_t)bucket * 4096 > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(fused_kernel<D, NT>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fused_kernel<D, NT, W>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, bucket * 4096) != hipSuccess) {
     (void)hipGetLastError();  // leave no error behind for the launch status check
     return 0;
   }
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, NT>, 64 * fused_waves<NT>(),
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, NT, W>, 64 * W,
                                                    (size_t)bucket * 4096) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
     (void)hipGetLastError();
     return 0;
   }
+#ifdef SDV_FUSED_MAX_PER_CU  // tuning builds: at most this many resident workgroups per CU
+  per_cu = min(per_cu, SDV_FUSED_MAX_PER_CU);
+#endif
   cap = per_cu * cus;
   cache[dev][bucket].store(cap, std::memory_order_relaxed);
   return cap;
@@ -1262,12 +1281,11 @@ struct FusedShape {
 // The single-launch shape: as many workgroups as the device holds at once (at most 64 items
 // per group, items of at least one page block), or false when the three-launch path must
 // serve the call (several query-row groups, too many groups, items too large for LDS).
-template <int D, int NT>
+template <int D, int NT, int W>
 static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
 #ifdef SDV_TUNE_NO_FUSED  // tuning builds only: always the three-launch path
   return false;
 #endif
-  constexpr int W = fused_waves<NT>();
   if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;
   const int G = (int)p.groups;
   const int gb = (max_seq_len + kBlock - 1) / kBlock;
@@ -1276,14 +1294,14 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
   const int max_items = min(min(kFusedMaxChunks, gb), max(1, gb / kFusedMinBlocks));
   // items whose fp32 partials fit the sync area
   const int part_cap = (int)(kSyncPartBytes / ((size_t)R * D * 4));
-  int cap = min(part_cap, fused_capacity<D, NT>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total));
+  int cap = min(part_cap, fused_capacity<D, NT, W>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total));
   for (int iter = 0; iter < 4; ++iter) {
     if (cap < G) return false;
     const int base = min(max_items, cap / G);
     const int maxblk = (gb + base - 1) / base;
     const size_t lds = (size_t)fused_lds_layout(R, D, maxblk, W, NT == 1).total;
     if (lds > 160 * 1024) return false;
-    const int cap2 = min(part_cap, fused_capacity<D, NT>(lds));
+    const int cap2 = min(part_cap, fused_capacity<D, NT, W>(lds));
     if (cap2 < cap) {  // a wider item needs more LDS: the device holds fewer of them
       cap = cap2;
       continue;
@@ -1304,13 +1322,14 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
 
 template <int D, int NT>
 static bool try_fused(AttnArgs a, const Plan& p, hipStream_t st) {
+  constexpr int W = fused_waves<D, NT>();
   FusedShape f;
-  if (!fused_shape<D, NT>(p, a.R, a.max_seq_len, &f)) return false;
+  if (!fused_shape<D, NT, W>(p, a.R, a.max_seq_len, &f)) return false;
   a.f_gb = f.gb;
   a.f_base = f.base;
   a.f_extra = f.extra;
   a.f_maxblk = f.maxblk;
-  hipLaunchKernelGGL((fused_kernel<D, NT>), dim3((unsigned)f.grid), dim3(64 * fused_waves<NT>()), f.lds, st, a);
+  hipLaunchKernelGGL((fused_kernel<D, NT, W>), dim3((unsigned)f.grid), dim3(64 * W), f.lds, st, a);
   return true;
 }
 
@@ -1320,10 +1339,10 @@ static int fused_grid_for(const Plan& p, int R, int max_seq_len) {
   FusedShape f;
   bool ok = false;
   switch (p.NT) {
-    case 1: ok = fused_shape<D, 1>(p, R, max_seq_len, &f); break;
-    case 2: ok = fused_shape<D, 2>(p, R, max_seq_len, &f); break;
-    case 3: ok = fused_shape<D, 3>(p, R, max_seq_len, &f); break;
-    default: ok = fused_shape<D, 4>(p, R, max_seq_len, &f); break;
+    case 1: ok = fused_shape<D, 1, fused_waves<D, 1>()>(p, R, max_seq_len, &f); break;
+    case 2: ok = fused_shape<D, 2, fused_waves<D, 2>()>(p, R, max_seq_len, &f); break;
+    case 3: ok = fused_shape<D, 3, fused_waves<D, 3>()>(p, R, max_seq_len, &f); break;
+    default: ok = fused_shape<D, 4, fused_waves<D, 4>()>(p, R, max_seq_len, &f); break;
   }
   return ok ? f.grid : 0;
 }

@@ -770,17 +770,40 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   }
   __syncthreads();
   float2* fs = sync_stats(a);
-  // the item's statistics of each row: lane l merges blocks l, l+64, ... in order, then a
-  // fixed xor tree over the 64 lanes -- independent of which wavefront took which block
-  for (int row = wave; row < a.R; row += W) {
+  // the item's statistics of each row, merged in an order that does not depend on which
+  // wavefront took which block in q.k^T.  One row per wavefront (decode): lane l merges
+  // blocks l, l+64, ... in order, then a fixed xor tree over the 64 lanes.  More rows
+  // (verify): the wavefront owns rows wave, wave + W, ... (rpw of them) and gives each a group
+  // of lpr lanes, so all its rows go through one pass (lane sl of a group merges blocks sl,
+  // sl + lpr, ... in order, then a fixed xor tree inside the group).
+  const int rpw = (a.R + W - 1) / W;  // <= 16: R <= 64 rows, W >= 4
+  if (rpw == 1) {
+    if (wave < a.R) {
+      float m = -INFINITY, l = 0.0f;
+      for (int j = lane; j < nbv; j += kWave) {
+        const float2 v = bst[j * a.R + wave];
+        merge_fast(m, l, v.x, v.y);
+      }
+#pragma unroll
+      for (int x = 1; x < kWave; x <<= 1) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));
+      if (lane == 0) store_dev_f2(fs + (int64_t)item * 64 + wave, make_float2(m, l));
+    }
+  } else {
+    const int lpr = rpw <= 2 ? 32 : rpw <= 4 ? 16 : rpw <= 8 ? 8 : 4;
+    const int sub = lane / lpr, sl = lane - sub * lpr;
+    const int row = wave + W * sub;
+    const bool act = sub < rpw && row < a.R;
     float m = -INFINITY, l = 0.0f;
-    for (int j = lane; j < nbv; j += kWave) {
-      const float2 v = bst[j * a.R + row];
-      merge_fast(m, l, v.x, v.y);
+    if (act) {
+      for (int j = sl; j < nbv; j += lpr) {
+        const float2 v = bst[j * a.R + row];
+        merge_fast(m, l, v.x, v.y);
+      }
     }
 #pragma unroll
-    for (int x = 1; x < kWave; x <<= 1) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));
-    if (lane == 0) store_dev_f2(fs + (int64_t)item * 64 + row, make_float2(m, l));
+    for (int x = 1; x < kWave / 2; x <<= 1)
+      if (x < lpr) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));  // wave-uniform
+    if (act && sl == 0) store_dev_f2(fs + (int64_t)item * 64 + row, make_float2(m, l));
   }
 
   // ------------------------------------------------------------------ 2. p.V
@@ -993,6 +1016,29 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
 
     group_stats(gm, ginv);
+    // The probabilities, once per (row, token) for all wavefronts: the item's scores in LDS
+    // become p = bf16(exp(s - M) / L) in place (a wavefront owns one dimension tile of every
+    // block, so forming p inside the p.V loop would repeat every exp once per tile).
+    // Masked (-inf) scores give p = 0.
+    {
+      const int nvec = nbv * (kBlock / 8);  // 8-score vectors per row
+      for (int e = tid; e < a.R * nvec; e += NTHR) {
+        const int row = e / nvec, v = e - row * nvec;
+        uint4* pp = reinterpret_cast<uint4*>(lsc + row * lrow + v * 8);
+        const float2 st = lgs[row];
+        const uint4 w4 = *pp;
+        const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
+        float pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
+          pr[i] = fast_exp(sc - st.x) * st.y;
+        }
+        *pp = make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
+                         pack_bf16x2(pr[6], pr[7]));
+      }
+    }
+    __syncthreads();
     f32x4 acc[DTW][NT];
   #pragma unroll
     for (int dtw = 0; dtw < DTW; ++dtw)
@@ -1022,19 +1068,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         bf16x8 pop[NT];
   #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          // rows past R and lane groups past the part see -inf scores: p = 0, never inf * 0
+          // rows past R and lane groups past the part take p = 0 (never inf * 0)
           const int row = nt * 16 + n;
-          uint4 w4 = make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u);
+          uint4 w4 = make_uint4(0u, 0u, 0u, 0u);
           if (in_part && row < a.R) w4 = *reinterpret_cast<const uint4*>(lsc + row * lrow + jb * kBlock + 8 * h);
-          const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
-          float pr[8];
-  #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
-            pr[i] = fast_exp(sc - gm[nt]) * ginv[nt];  // masked (-inf) scores -> 0
-          }
-          pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                                                          pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+          pop[nt] = __builtin_bit_cast(bf16x8, w4);
         }
         float sv[8];
         if (h == 0) {

@@ -1244,17 +1244,19 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   const int64_t units = (int64_t)L * B * KV * p->n_row_groups;
   const int64_t blocks = units * ((max_seq_len + kBlock - 1) / kBlock);
   // About one resident round of workgroups (4 per CU for qk, 2 for pv); each wavefront
-  // then streams its blocks through the load pipeline.
+  // then streams its blocks through the load pipeline.  Large problems give pv wavefronts
+  // up to 64 blocks (measured on config 4, B=32 x 28 layers: p.V 1187 us at 32 -> 1037 us at
+  // 64); 64 is also the most pv_kernel can take: it holds one page id per lane.
   int qb = 1;
   const int qb_max = kQkScoreTokens / (kBlock * p->NT) >= 1 ? kQkScoreTokens / (kBlock * p->NT) : 1;
   while (qb < qb_max && blocks > (int64_t)kWaves * qb * 1024) qb *= 2;
   int pb = 4;  // multiple of the 4-block pv stage
-  while (pb < 32 && blocks > (int64_t)kWaves * pb * 512) pb *= 2;
+  while (pb < kWave && blocks > (int64_t)kWaves * pb * 512) pb *= 2;
 #ifdef SDV_TUNE_QK_BPW  // tuning builds only: fixed blocks per wavefront
   qb = min(SDV_TUNE_QK_BPW, qb_max);
 #endif
 #ifdef SDV_TUNE_PV_BPW
-  pb = (SDV_TUNE_PV_BPW + 3) / 4 * 4;
+  pb = min((SDV_TUNE_PV_BPW + 3) / 4 * 4, kWave);
 #endif
   p->qk_bpw = qb;
   p->qk_chunk_tokens = kWaves * qb * kBlock;

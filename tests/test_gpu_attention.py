@@ -306,3 +306,17 @@ def test_multi_layer_batch32_ragged(cuda_device):
     fp = cache.footprint()
     assert fp["tokens"] == sum(lens)
     assert abs(fp["saved_frac"] - (1 - 776 / 1024)) < 1e-9
+
+
+@pytest.mark.parametrize("h,d,s,t,layers", [(12, 128, 8, 3000, 1), (12, 128, 10, 1500, 1), (14, 64, 5, 2048, 1),
+                                            (12, 128, 8, 4096, 4), (14, 64, 5, 4096, 6)])
+def test_single_launch_three_and_four_row_tiles(cuda_device, h, d, s, t, layers):
+    """Query-row groups of 3 and 4 MFMA row tiles (R = G*S = 48, 60, 35 rows) on the single
+    launch: probabilities formed once per item in LDS, statistics of several rows per
+    wavefront merged in one pass."""
+    announce(f"attn single launch {h}/2/{d} S={s} T={t} L={layers}")
+    r = (h // 2) * s
+    assert r > 32, r  # three or four row tiles
+    assert ops.single_launch_workgroups(layers, 1, h, 2, s, d, t) > 0
+    cache = _filled_cache(cuda_device, layers, 2, d, [t], seed=600 + s + t)
+    _check_multi_layer(cuda_device, cache, h, s, tuple(sorted({0, layers - 1})), (0,), f"{h}/{d} S={s}", seed=601)

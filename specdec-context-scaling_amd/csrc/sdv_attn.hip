@@ -614,8 +614,9 @@ __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, i
   l.gstats = (l.pages + maxblk * 4 + 15) & ~15;                           // [64] float2
   l.parts = l.gstats + 64 * 8;
   l.total = l.parts + (claim_pv ? (maxblk + 3) / 4 : (tp > 1 ? tp : 0)) * R * D * 4;
-  l.red = 0;  // output stage, after p.V: one 16-byte chunk per (item, owned chunk)
-  const int red_bytes = (R * D / 4 + kFusedMaxChunks) * 16;
+  l.red = 0;  // output stage, after p.V: one 16-byte chunk per (item, owned chunk), then one
+              // per (segment of items, owned chunk): at most one per thread
+  const int red_bytes = (R * D / 4 + kFusedMaxChunks + 64 * W) * 16;
   if (l.total < red_bytes) l.total = red_bytes;
   return l;
 }
@@ -784,8 +785,14 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         const float2 v = bst[j * a.R + wave];
         merge_fast(m, l, v.x, v.y);
       }
+      if (nbv >= kWave) {
 #pragma unroll
-      for (int x = 1; x < kWave; x <<= 1) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));
+        for (int x = 1; x < kWave; x <<= 1) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));
+      } else {  // lanes >= nbv hold nothing: the tree only needs to span the first nbv lanes
+#pragma unroll
+        for (int x = 1; x < kWave; x <<= 1)
+          if (x < nbv) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));  // wave-uniform
+      }
       if (lane == 0) store_dev_f2(fs + (int64_t)item * 64 + wave, make_float2(m, l));
     }
   } else {
@@ -1177,22 +1184,55 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     if (act) red[e] = part_dec(v);
   }
   __syncthreads();
-  // sum over the items in item order; the LDS reads go out eight at a time ahead of the
-  // adds (a plain loop is one dependent LDS round trip per item)
+  // Sum over the items in a fixed order.  For 16 items or more and enough threads, in two
+  // levels: thread (sg, o) adds the items of segment sg (about sqrt(nvq) of them) in order,
+  // then thread o adds the segments in order; one thread per chunk would walk a dependent
+  // chain of nvq LDS reads (one layer at T=8192: 64 items, 1.7 us).
+  // nseg > 1 implies nseg * w <= NTHR, the size of the segment area after the item chunks.
+  float4* red2 = red + nld;
+  int nseg = 1;
+  while (nseg * nseg < nvq) ++nseg;
+  nseg = (w > 0 && nvq >= 16) ? min(nseg, NTHR / w) : 1;  // short chains: one level is cheaper
+  const int segsz = nseg > 1 ? (nvq + nseg - 1) / nseg : nvq;
+  if (nseg > 1) {
+    for (int t = tid; t < nseg * w; t += NTHR) {
+      const int sg = t / w, o = t - sg * w;
+      const int c0 = sg * segsz, c1 = min(nvq, c0 + segsz);
+      float4 sm = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      int cc = c0;
+      for (; cc + 4 <= c1; cc += 4) {
+        float4 f[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) f[k] = red[(cc + k) * w + o];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sm.x += f[k].x; sm.y += f[k].y; sm.z += f[k].z; sm.w += f[k].w;
+        }
+      }
+      for (; cc < c1; ++cc) {
+        const float4 f = red[cc * w + o];
+        sm.x += f.x; sm.y += f.y; sm.z += f.z; sm.w += f.w;
+      }
+      red2[t] = sm;
+    }
+    __syncthreads();
+  }
+  const float4* src = nseg > 1 ? red2 : red;  // [part][chunk]: parts added in order below
+  const int nsrc = nseg > 1 ? nseg : nvq;
   for (int o = tid; o < w; o += NTHR) {
-    float4 sm = red[o];
+    float4 sm = src[o];
     int cc = 1;
-    for (; cc + 8 <= nvq; cc += 8) {
+    for (; cc + 8 <= nsrc; cc += 8) {
       float4 f[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) f[k] = red[(cc + k) * w + o];
+      for (int k = 0; k < 8; ++k) f[k] = src[(cc + k) * w + o];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         sm.x += f[k].x; sm.y += f[k].y; sm.z += f[k].z; sm.w += f[k].w;
       }
     }
-    for (; cc < nvq; ++cc) {
-      const float4 f = red[cc * w + o];
+    for (; cc < nsrc; ++cc) {
+      const float4 f = src[cc * w + o];
       sm.x += f.x; sm.y += f.y; sm.z += f.z; sm.w += f.w;
     }
     const int o4 = lo + o;

@@ -523,8 +523,9 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
 // One launch for the shapes whose whole grid fits the device at once (one query-row group:
 // decode and verify).  One workgroup per CU (W = 8 or 16 wavefronts for decode; 8 or 4 when
 // the row tiles need more registers), each owning one item: a run of page blocks of one
-// (layer*batch, KV head) group.  Groups are cut into items of nearly equal size (a group
-// gets f_base or f_base+1 items), so every CU streams the same number of bytes.  Inside a
+// (layer*batch, KV head) group.  Every group is cut into the same number of items of nearly
+// equal size (the kernel also takes f_base+1 items for the first f_extra groups, which the
+// planner no longer uses), so every busy CU streams the same number of bytes.  Inside a
 // workgroup the wavefronts claim page blocks from an LDS counter, so a wavefront the
 // scheduler favours takes more blocks and all finish together.  Per workgroup:
 //   1. q.k^T over the item's blocks: BF16 scores and per-block (max, sum) of every row into
@@ -1386,7 +1387,11 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
       cap = cap2;
       continue;
     }
-    const int extra = base < max_items ? min(G - 1, cap - G * base) : 0;
+    // Every group gets the same number of items, even if some CUs stay idle: extra items
+    // would only shrink the items of some groups, while the largest items set the end of the
+    // call, and the workgroups left with them stream alone at the end.  Measured on 28 layers
+    // at 8K: 224 equal items 39.4 us against 256 mixed items (102 and 128 blocks) 41.2 us.
+    const int extra = 0;
     const int grid = G * base + extra;
     if (grid > kFusedMaxItems || grid > part_cap) return false;
     f->gb = gb;

@@ -340,7 +340,10 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
     for t in (2048, 4096, 8192):
         row = attn_rows(dreps, dL, dH, dKV, dD, t, 1, f"cfg3_draft_decode_T{t}")
         row["five_decodes_us"] = round(5 * row["per_layer_calls_us_per_layer"] * dL, 1)
+    _progress("cfg3 chains")
+    out["cfg3_draft_chain_5x24_T8192"] = chain_row(torch, dev, dreps, dL, dH, dKV, dD, 8192, 1, 5)
     del dreps
+    out["cfg3_target_verify_step_28_T8192"] = chain_row(torch, dev, reps8k, L, H, KV, D, 8192, 5, 1)
     # config 4: B=32 ragged contexts U{2048..32768}, fragmented pool, 1% outlier channels x20
     lens = wl.ragged_lengths(32, 2048, 32768, seed=41)
     creps = _build(torch, dev, L, KV, D, lens, 1, seed0=4000, outliers=True)
@@ -376,6 +379,65 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
         _progress("cpu rows")
         out["cpu"] = cpu_rows(budget_s=2.0)
     return out
+
+
+def chain_row(torch, dev, reps, layers, h, kv, d, T, s, steps):
+    """The engine's per-layer call pattern for `steps` speculative steps, in one HIP graph: per
+    step and layer, kernel 1 appends the step's s new tokens (BF16 K copy and FP8 V) at the end
+    of the context, then the layer's attention runs over it (T tokens after the last step).
+    Draft chain: s=1, 5 steps; target verify: s=5, 1 step."""
+    from specdec_amd import workloads as wl
+    from specdec_amd.kernels import ops
+
+    ws = ops.new_workspace(dev, ops.attention_workspace_bytes(1, 1, h, kv, s, d, T))
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    per = []
+    for r in reps:
+        c = r["cache"]
+        k_new = torch.randn((steps, layers, s, kv, d), generator=g, device=dev).to(torch.bfloat16)
+        v_new = torch.randn((steps, layers, s, kv, d), generator=g, device=dev).to(torch.bfloat16)
+        q = torch.randn((steps, layers, 1, h, s, d), generator=g, device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q[0, 0])
+        starts = [T - s * (steps - j) for j in range(steps)]
+        slots = [c.slot_mapping([p0], s) for p0 in starts]
+        lens = [torch.full((1,), p0 + s, dtype=torch.int32, device=dev) for p0 in starts]
+        per.append((c, k_new, v_new, q, out, slots, lens, r["bt"]))
+
+    def chain(ri):
+        c, k_new, v_new, q, out, slots, lens, bt = per[ri]
+        for j in range(steps):
+            for layer in range(layers):
+                kp, vp, vs = c.layer(layer)
+                ops.quant_append(v_new[j, layer], slots[j], kp, vp, vs, k_new[j, layer])
+                ops.paged_attention(q[j, layer], kp, vp, vs, bt, lens[j], T, out=out, workspace_tensor=ws)
+
+    # the graph-capture helper replays several chains per graph; keep the graph small
+    us = _time_chain(torch, chain, len(reps))
+    nbytes = steps * layers * (wl.bytes_attn(T, s, h, kv, d) + wl.bytes_quant_append(s, kv, d, True))
+    return {"layers": layers, "steps": steps, "q_len": s, "T": T, "launches": 2 * steps * layers,
+            "us_per_chain": round(us, 1), "us_per_layer_step": round(us / (steps * layers), 3),
+            "GBps": _gbs(nbytes, us)}
+
+
+def _time_chain(torch, chain, nrep, replays=6):
+    """Average us of chain(r): one HIP graph holding one chain per replica, replayed."""
+    graph = torch.cuda.CUDAGraph()
+    for r in range(nrep):
+        chain(r)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for r in range(nrep):
+            chain(r)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (replays * nrep)
 
 
 class _LayerView:

@@ -19,6 +19,7 @@ Operators
 from __future__ import annotations
 
 import ctypes
+import functools
 import weakref
 
 import torch
@@ -38,18 +39,26 @@ def _fail(msg: str):
     raise SdvError(msg, _native.SDV_ERR_SHAPE)
 
 
-def _stream(dev: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+# The eager engine calls these operators once per layer and step, so their host cost is part of
+# every decoded token: pointers go to ctypes as plain ints (the argtypes are c_void_p), the
+# current stream comes from torch's raw query when it has one, and workspace sizes are cached.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(dev: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 def _p(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    return t.data_ptr() if t is not None else None
 
 
 def _need(t, name, dtypes, dev=None, ndim=None):
     if not isinstance(t, torch.Tensor):
         _fail(f"{name} must be a tensor")
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         _fail(f"{name} must be on a HIP device (got {t.device})")
     if dev is not None and t.device != dev:
         _fail(f"{name} is on {t.device}, expected {dev}")
@@ -96,7 +105,7 @@ def _init_workspace(ws: torch.Tensor) -> None:
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A cached uint8 workspace of at least nbytes on (device, current stream)."""
     dev = torch.device(device)
-    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    key = (dev, _stream(dev))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = new_workspace(dev, max(nbytes, 1 << 20))
@@ -117,6 +126,7 @@ def sync_errors(ws: torch.Tensor) -> int:
     return int(ws[:4].view(torch.int32).item())
 
 
+@functools.lru_cache(maxsize=256)
 def attention_workspace_bytes(num_layers: int, batch: int, q_heads: int, kv_heads: int, q_len: int,
                               head_dim: int, max_seq_len: int) -> int:
     n = _native.load().sdv_attention_workspace_size(num_layers, batch, q_heads, kv_heads, q_len,

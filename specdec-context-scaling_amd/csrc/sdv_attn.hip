@@ -192,13 +192,15 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
   // The prefetch is unconditional (a stage past the end reads block 0, which every wave of
   // the layer shares in L2, and is masked): conditional loads would make the wait counters
   // at the loop head imprecise and serialize the pipeline.
+  // The loop has one exit, at its head, and reloads both buffers unconditionally, so every
+  // path into the head has the same loads pending (a break between the two halves would
+  // merge the other buffer's pending loads into the head and make the compiler wait there).
   if (nb > 0) load_stage(0, ka, pa);
   for (int j0 = 0; j0 < nb; j0 += 2 * P) {
     load_stage(j0 + P, kb, pbb);
     compute_stage(ka, pa, j0);
-    if (j0 + P >= nb) break;
     load_stage(j0 + 2 * P, ka, pa);
-    compute_stage(kb, pbb, j0 + P);
+    compute_stage(kb, pbb, j0 + P);  // nothing past nb
   }
 
 #pragma unroll
@@ -535,8 +537,9 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
 //      yet": no counter is needed for this step.
 //   2. Once every non-empty item of the group has published (one wavefront polls, the
 //      others keep their first V loads in flight), the group's statistics are merged in a
-//      fixed order; the wavefronts run p.V over the item's blocks; per-unit results are
-//      summed in LDS in order and the fp32 partial is published.
+//      fixed order; the item's scores in LDS become p = bf16(exp(s - M) / L) in place, once
+//      per (row, token); the wavefronts run p.V over the item's blocks; per-unit results
+//      are summed in LDS in order and the fp32 partial is published.
 //   3. Workgroup c of the group owns a slice of the outputs: it polls the slice of every
 //      item's partial (a published partial word is its bits + 1, so zero means "not yet"),
 //      sums it over the items in order (the result does not depend on the order workgroups
@@ -556,6 +559,10 @@ constexpr int kFusedMaxChunks = 64;     // items per group
 #define SDV_FUSED_MIN_BLOCKS 1
 #endif
 constexpr int kFusedMinBlocks = SDV_FUSED_MIN_BLOCKS;
+#ifndef SDV_FUSED_MAX_PER_CU  // tuning builds: resident decode workgroups per CU
+#define SDV_FUSED_MAX_PER_CU 1
+#endif
+constexpr int kFusedMaxPerCU = SDV_FUSED_MAX_PER_CU;
 constexpr size_t kSyncHeadBytes = 256;  // word 0: expired waits
 constexpr size_t kSyncStatsBytes = (size_t)kFusedMaxItems * 64 * 8;
 constexpr size_t kSyncPartBytes = (size_t)8 << 20;  // fp32 partials of one call's items
@@ -756,18 +763,24 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         }
       }
     };
+    // Two claims in flight per wavefront.  The loop has one exit, at its head, and both
+    // stages are reloaded unconditionally (an exhausted claim reads block 0, an L2 hit), so
+    // every path into the head has the same loads pending.  A break between the stages
+    // would merge the other stage's pending loads into the head, and the compiler then
+    // waits there for all loads before the next claim (one block in flight instead of two).
     bf16x8 ka[P][KK], kb[P][KK];
     int pa[P], pbb[P];
     int ja = claim();
     load_stage(ja, ka, pa);
-    while (ja < nbv) {
+    bool more = ja < nbv;
+    while (more) {
       const int jb2 = claim();
       load_stage(jb2, kb, pbb);
       compute_stage(ka, pa, ja);
-      if (jb2 >= nbv) break;
       ja = claim();
       load_stage(ja, ka, pa);
-      compute_stage(kb, pbb, jb2);
+      compute_stage(kb, pbb, jb2);  // nothing when jb2 >= nbv
+      more = ja < nbv;              // claims increase: ja < nbv implies jb2 < nbv
     }
   }
   __syncthreads();
@@ -877,6 +890,29 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     }
   };
 
+  // The probabilities, once per (row, token) for all wavefronts: the item's scores in LDS
+  // become p = bf16(exp(s - M) / L) in place (with several row tiles a wavefront owns one
+  // dimension tile of every block, so forming p inside the p.V loop would repeat every exp
+  // once per tile).  Masked (-inf) scores give p = 0.  Needs the group statistics in LDS.
+  auto prob_pass = [&]() {
+    const int nvec = nbv * (kBlock / 8);  // 8-score vectors per row
+    for (int e = tid; e < a.R * nvec; e += NTHR) {
+      const int row = e / nvec, v = e - row * nvec;
+      uint4* pp = reinterpret_cast<uint4*>(lsc + row * lrow + v * 8);
+      const float2 st = lgs[row];
+      const uint4 w4 = *pp;
+      const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
+      float pr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
+        pr[i] = fast_exp(sc - st.x) * st.y;
+      }
+      *pp = make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
+                       pack_bf16x2(pr[6], pr[7]));
+    }
+  };
+
   float gm[NT], ginv[NT];
   if constexpr (kClaimPV) {
     // Units of (4 blocks, up to 4 dimension tiles), claimed from an LDS counter so that all
@@ -932,18 +968,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       for (int t = 0; t < UT; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        // rows past R and lane groups past the item see -inf scores: p = 0, never inf * 0
-        uint4 w4 = make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u);
+        // the probabilities of the block (formed once in LDS); rows past R and lane groups
+        // past the item take p = 0 (never inf * 0)
+        uint4 w4 = make_uint4(0u, 0u, 0u, 0u);
         if (jb < nbv && n < a.R) w4 = *reinterpret_cast<const uint4*>(lsc + n * lrow + jb * kBlock + 8 * h);
-        const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
-        float pr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
-          pr[i] = fast_exp(sc - gm[0]) * ginv[0];
-        }
-        const bf16x8 pop = __builtin_bit_cast(bf16x8, make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                                                                 pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+        const bf16x8 pop = __builtin_bit_cast(bf16x8, w4);
         float sv[8];
         if (h == 0) {
           sv[0] = row_bcast<0>(x.scl); sv[1] = row_bcast<1>(x.scl); sv[2] = row_bcast<2>(x.scl);
@@ -975,18 +1004,25 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
           *reinterpret_cast<f32x4*>(lparts + ((k * a.R + n) * D + hf * UT * 16 + t * 16 + 4 * g)) = acc[t];
       }
     };
+    // two units in flight per wavefront; one loop exit, at the head (as in q.k^T)
     Unit ua, ub;
     int u0 = claim2();
     load_u(u0, ua);
     group_stats(gm, ginv);
-    while (u0 < nunits) {
+    // p formed once per (row, token) before the loop: a unit covers half the dimensions of
+    // its blocks, so forming p per unit would repeat every exp (28 layers at 8K: 39.2 ->
+    // 37.2 us together with the single-exit loops)
+    prob_pass();
+    __syncthreads();
+    bool more = u0 < nunits;
+    while (more) {
       const int u1 = claim2();
       load_u(u1, ub);
       compute_u(u0, ua);
-      if (u1 >= nunits) break;
       u0 = claim2();
       load_u(u0, ua);
-      compute_u(u1, ub);
+      if (u1 < nunits) compute_u(u1, ub);  // wave-uniform
+      more = u0 < nunits;
     }
     __syncthreads();
     // the item's partial: unit slots summed in stage order
@@ -1024,28 +1060,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
 
     group_stats(gm, ginv);
-    // The probabilities, once per (row, token) for all wavefronts: the item's scores in LDS
-    // become p = bf16(exp(s - M) / L) in place (a wavefront owns one dimension tile of every
-    // block, so forming p inside the p.V loop would repeat every exp once per tile).
-    // Masked (-inf) scores give p = 0.
-    {
-      const int nvec = nbv * (kBlock / 8);  // 8-score vectors per row
-      for (int e = tid; e < a.R * nvec; e += NTHR) {
-        const int row = e / nvec, v = e - row * nvec;
-        uint4* pp = reinterpret_cast<uint4*>(lsc + row * lrow + v * 8);
-        const float2 st = lgs[row];
-        const uint4 w4 = *pp;
-        const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
-        float pr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
-          pr[i] = fast_exp(sc - st.x) * st.y;
-        }
-        *pp = make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
-                         pack_bf16x2(pr[6], pr[7]));
-      }
-    }
+    prob_pass();
     __syncthreads();
     f32x4 acc[DTW][NT];
   #pragma unroll
@@ -1109,11 +1124,14 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         }
       }
     };
+    // one loop exit, at the head, and unconditional reloads: every path into the head has
+    // the ring's loads pending in ring order, so stage i waits only for its own loads (a
+    // break after stage i would reorder the pending loads of the merged paths and make the
+    // compiler wait for nearly the whole ring before stage 0)
     for (int st0 = 0; st0 < nstage; st0 += SD) {
   #pragma unroll
       for (int i = 0; i < SD; ++i) {
-        if (st0 + i >= nstage) break;
-        compute_v(st0 + i, ring[i]);
+        if (st0 + i < nstage) compute_v(st0 + i, ring[i]);  // wave-uniform
         load_v(st0 + i + SD, ring[i]);
       }
     }
@@ -1346,9 +1364,10 @@ static int fused_capacity(size_t lds) {
     (void)hipGetLastError();
     return 0;
   }
-#ifdef SDV_FUSED_MAX_PER_CU  // tuning builds: at most this many resident workgroups per CU
-  per_cu = min(per_cu, SDV_FUSED_MAX_PER_CU);
-#endif
+  // Decode (one row tile): one workgroup per CU, whatever the register count would allow.  A
+  // second resident workgroup only splits the CU's bandwidth between two items of the same
+  // size (measured on 28 layers at 8K: 504 workgroups 42.7-43.1 us against 224 at 39.4 us).
+  if (NT == 1) per_cu = min(per_cu, kFusedMaxPerCU);
   cap = per_cu * cus;
   cache[dev][bucket].store(cap, std::memory_order_relaxed);
   return cap;

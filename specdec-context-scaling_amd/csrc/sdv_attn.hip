@@ -84,6 +84,22 @@ __device__ __forceinline__ void merge_fast(float& m, float& l, float m2, float l
   m = mn;
   l = a + b;
 }
+// Merges of (max, sum) across lanes without LDS.  merge_fast is symmetric in its two operands
+// (max, two products, one sum: no contraction across the selects), so both lanes of a pair
+// get identical bits.
+// merge with the lane X apart, X = 16 or 32: every lane gets merge(lower lane, upper lane)
+template <int X>
+__device__ __forceinline__ void merge_lanes(float& m, float& l) {
+  const float2 mm = lane_pair<X>(m), ll = lane_pair<X>(l);
+  m = mm.x;
+  l = ll.x;
+  merge_fast(m, l, mm.y, ll.y);
+}
+// merge with lane (lane ^ X), X = 1, 2, 4, 8: valid for the lanes lane_xor_low<X> serves
+template <int X>
+__device__ __forceinline__ void merge_xor_low(float& m, float& l) {
+  merge_fast(m, l, lane_xor_low<X>(m), lane_xor_low<X>(l));
+}
 
 // ---------------------------------------------------------------------------- q.k^T
 template <int D, int NT>
@@ -206,8 +222,8 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float m = m_run[nt], l = l_run[nt];
-    merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
-    merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+    merge_lanes<16>(m, l);
+    merge_lanes<32>(m, l);
     if (g == 0) lstat[wave][nt * 16 + n] = make_float2(m, l);
   }
   __syncthreads();
@@ -441,8 +457,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SDV_PV_WAVE
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float m = sm[nt], l = sl[nt];
-    merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
-    merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+    merge_lanes<16>(m, l);
+    merge_lanes<32>(m, l);
     gm[nt] = m;
     ginv[nt] = 1.0f / l;
   }
@@ -757,8 +773,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
             for (int i = 0; i < 4; ++i) l += fast_exp(s4[i] - mt);
           }
           float m = mt;
-          merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
-          merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+          merge_lanes<16>(m, l);
+          merge_lanes<32>(m, l);
           if (g == 0 && row < a.R) bst[jb * a.R + row] = make_float2(m, l);
         }
       }
@@ -799,14 +815,15 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         const float2 v = bst[j * a.R + wave];
         merge_fast(m, l, v.x, v.y);
       }
-      if (nbv >= kWave) {
-#pragma unroll
-        for (int x = 1; x < kWave; x <<= 1) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));
-      } else {  // lanes >= nbv hold nothing: the tree only needs to span the first nbv lanes
-#pragma unroll
-        for (int x = 1; x < kWave; x <<= 1)
-          if (x < nbv) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));  // wave-uniform
-      }
+      // a fixed tree whose result lane 0 holds: lane 0 takes lanes 1, 2, 4 and 8 (row shifts
+      // and quad permutes), then rows 16 and 32 apart.  Lanes >= nbv hold nothing, so the tree
+      // only needs to span the first nbv lanes (wave-uniform tests).
+      if (nbv > 1) merge_xor_low<1>(m, l);
+      if (nbv > 2) merge_xor_low<2>(m, l);
+      if (nbv > 4) merge_xor_low<4>(m, l);
+      if (nbv > 8) merge_xor_low<8>(m, l);
+      if (nbv > 16) merge_lanes<16>(m, l);
+      if (nbv > 32) merge_lanes<32>(m, l);
       if (lane == 0) store_dev_f2(fs + (int64_t)item * 64 + wave, make_float2(m, l));
     }
   } else {
@@ -821,9 +838,13 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         merge_fast(m, l, v.x, v.y);
       }
     }
-#pragma unroll
-    for (int x = 1; x < kWave / 2; x <<= 1)
-      if (x < lpr) merge_fast(m, l, xor_lane(m, x), xor_lane(l, x));  // wave-uniform
+    // the group leaders (sl = 0: lanes that are multiples of lpr) take lanes 1, 2, 4, 8 and 16
+    // apart, as far as the group reaches (wave-uniform tests)
+    merge_xor_low<1>(m, l);
+    merge_xor_low<2>(m, l);
+    if (lpr > 4) merge_xor_low<4>(m, l);
+    if (lpr > 8) merge_xor_low<8>(m, l);
+    if (lpr > 16) merge_lanes<16>(m, l);
     if (act && sl == 0) store_dev_f2(fs + (int64_t)item * 64 + row, make_float2(m, l));
   }
 
@@ -875,8 +896,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
             }
           }
         }
-        merge_fast(m, l, xor_lane(m, 16), xor_lane(l, 16));
-        merge_fast(m, l, xor_lane(m, 32), xor_lane(l, 32));
+        merge_lanes<16>(m, l);
+        merge_lanes<32>(m, l);
         if (g == 0 && rr < a.R) lgs[rr] = make_float2(m, 1.0f / l);
       }
     }

@@ -105,10 +105,30 @@ __device__ __forceinline__ uint32_t wave_max_nonneg_bits(uint32_t v) {
   return max(max(r0, r1), max(r2, r3));
 }
 
-// Exchange with the lane `mask` apart (mask in {16, 32}: across 16-lane rows).
-__device__ __forceinline__ float xor_lane(float v, int mask) {
-  const int src = (int)(threadIdx.x & 63) ^ mask;
-  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+// Lane exchanges without an LDS round trip.  lane_xor_low<X>: the value of lane (lane ^ X) --
+// for every lane when X = 1 or 2 (quad permutes), and for the lanes whose bit X is clear when
+// X = 4 or 8 (DPP row shift left: lane i reads lane i + X of its 16-lane row; the lanes past
+// the row's end read 0).
+template <int X>
+__device__ __forceinline__ float lane_xor_low(float v) {
+  static_assert(X == 1 || X == 2 || X == 4 || X == 8, "quad permutes and row shifts only");
+  constexpr int ctrl = X == 1 ? 0xB1 : X == 2 ? 0x4E : X == 4 ? 0x104 : 0x108;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+// lane_pair<X>, X = 16 or 32: the values of the two lanes X apart that this lane belongs to,
+// lower lane first (rows 2k and 2k+1 of 16 lanes, or the two halves of 32), the same pair in
+// both lanes (gfx950 v_permlane16_swap / v_permlane32_swap).
+template <int X>
+__device__ __forceinline__ float2 lane_pair(float v) {
+  static_assert(X == 16 || X == 32, "row pairs or wave halves");
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (X == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
 }
 
 // Online-softmax statistic merge: (m, l) with l = sum exp(s - m); m = -inf means empty.

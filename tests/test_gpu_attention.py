@@ -287,6 +287,26 @@ def test_multi_layer_draft_d64(cuda_device):
     _check_multi_layer(cuda_device, cache, 14, 1, (0, 13, 23), (0,), "draft", seed=502)
 
 
+def test_multi_layer_decode_28(cuda_device):
+    """The headline decode shape (28 layers, 12/2/128, T=8192) in one launch, checked on the
+    first, two middle and the last layer."""
+    announce("attn multi-layer decode 28x12/2/128 T=8192")
+    cache = _filled_cache(cuda_device, 28, 2, 128, [8192], seed=530)
+    _check_multi_layer(cuda_device, cache, 12, 1, (0, 13, 14, 27), (0,), "decode 28L", seed=531)
+
+
+@pytest.mark.parametrize("layers,kv,h,lens", [(37, 1, 6, [7000]), (8, 2, 12, [8192, 3000, 17])])
+def test_single_launch_odd_groups_and_ragged(cuda_device, layers, kv, h, lens):
+    """The single launch with an odd number of groups (37 layers, one KV head) and with ragged
+    sequences in one batch (items past a short sequence's end own nothing)."""
+    announce(f"attn single launch L={layers} kv={kv} h={h} lens={lens}")
+    assert ops.single_launch_workgroups(layers, len(lens), h, kv, 1, 128, max(lens)) > 0
+    cache = _filled_cache(cuda_device, layers, kv, 128, lens, seed=540 + layers)
+    seqs = tuple(range(len(lens)))
+    _check_multi_layer(cuda_device, cache, h, 1, tuple(sorted({0, layers // 2, layers - 1})), seqs,
+                       f"L={layers} lens={lens}", seed=541)
+
+
 @pytest.mark.parametrize("t", [2048, 8192])
 def test_multi_layer_verify_s5(cuda_device, t):
     """The k+1=5-row verify over all 28 target layers in one launch."""

@@ -622,6 +622,10 @@ __device__ __forceinline__ float4 part_dec(u32x4_t w) {
 template <int D, int NT>
 constexpr int fused_waves() { return NT == 1 ? (D == 128 ? 8 : 16) : NT == 2 ? 8 : 4; }
 constexpr int kVStages = 6;  // p.V stages in flight per wavefront
+// dimension-tile groups of the static p.V split (several row tiles): wavefront w takes the
+// 16-dimension tiles of group w % ntg for block part w / ntg (measured on 28-layer verify at
+// 8K: 2 or 4 groups of wider tiles, with 3 to 6 stages, no faster than one tile per wavefront)
+__host__ __device__ constexpr int fused_ntg(int D, int W) { return D / 16 < W ? D / 16 : W; }
 
 // dynamic LDS of a fused workgroup with items of up to `maxblk` blocks (byte offsets).  With
 // one row tile the p.V work is claimed in units and each unit's result gets an LDS slot
@@ -630,14 +634,23 @@ struct FusedLds {
   int scores, bstats, pages, gstats, parts, red, total;
 };
 __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool claim_pv) {
-  const int DT = D / 16, ntg = DT < W ? DT : W, tp = W / ntg;
+  const int ntg = fused_ntg(D, W), tp = W / ntg;
   FusedLds l;
   l.scores = 0;                                                            // [R][16*maxblk + 8] bf16
   l.bstats = (l.scores + R * (maxblk * kBlock + 8) * 2 + 15) & ~15;        // [maxblk][R] float2
   l.pages = l.bstats + maxblk * R * 8;                                     // [maxblk] int
   l.gstats = (l.pages + maxblk * 4 + 15) & ~15;                           // [64] float2
-  l.parts = l.gstats + 64 * 8;
-  l.total = l.parts + (claim_pv ? (maxblk + 3) / 4 : (tp > 1 ? tp : 0)) * R * D * 4;
+  if (claim_pv) {
+    l.parts = l.gstats + 64 * 8;
+    l.total = l.parts + (maxblk + 3) / 4 * R * D * 4;
+  } else {
+    // the static split's parts are written after every wavefront has finished p.V: they
+    // reuse the scores from offset 0
+    l.parts = 0;
+    l.total = l.gstats + 64 * 8;
+    const int parts_bytes = (tp > 1 ? tp : 0) * R * D * 4;
+    if (l.total < parts_bytes) l.total = parts_bytes;
+  }
   l.red = 0;  // output stage, after p.V: one 16-byte chunk per (item, owned chunk), then one
               // per (segment of items, owned chunk): at most one per thread
   const int red_bytes = (R * D / 4 + kFusedMaxChunks + 64 * W) * 16;
@@ -649,7 +662,7 @@ template <int D, int NT, int W>
 __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   constexpr int NTHR = 64 * W;
   constexpr int KK = D / 32, DT = D / 16;
-  constexpr int NTG = DT < W ? DT : W;   // dimension-tile groups in p.V
+  constexpr int NTG = fused_ntg(D, W);  // dimension-tile groups in p.V
   constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
   constexpr int TP = W / NTG;            // block parts in p.V
 #ifndef SDV_TUNE_QK_CLAIM
@@ -1159,6 +1172,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
 
     // lane (g, n) holds rows nt*16+n, dims tg*DTW*16 + dtw*16 + 4g .. +3; parts summed in order
     if (TP > 1) {
+      __syncthreads();  // the parts overwrite the probabilities the other wavefronts read
   #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int row = nt * 16 + n;

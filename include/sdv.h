@@ -29,6 +29,9 @@
  *                           -> pybind attention (specdec/kernels/cuda/bind.cpp:16)
  *                           -> attention_cuda (specdec/kernels/cuda/attention.cu:244-288)
  *                           computes, with FP8 V dequantized inside the kernel
+ *   sdv_quant_append_tiles <- no counterpart: sdv_quant_append for the engine's batched
+ *                           varlen prefill (a table of 16-row tiles that follow each
+ *                           sequence's start)
  *   sdv_attention_workspace_size  <- no counterpart (the reference allocates its score,
  *                           softmax and kv_repeat temporaries inside torch)
  *   sdv_fp8_encode       <- the tensor.to(torch.float8_e4m3fn) cast (model_self.py:312)
@@ -81,6 +84,22 @@ int sdv_quant_append(const void* v_new, const void* k_new, const int32_t* slot_m
                      void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
                      int64_t k_layer_stride, int64_t v_layer_stride, int64_t s_layer_stride,
                      int32_t scale_mode, void* stream);
+
+/*
+ * sdv_quant_append with a tile table: tile i is input rows [tile_starts[i],
+ * min(tile_starts[i] + 16, tile_starts[i+1])) (n_tiles + 1 entries, non-decreasing, within
+ * [0, n_tokens]; rows that no tile covers are not written).  Same results as
+ * sdv_quant_append for any table that covers every row once.  No counterpart in the reference
+ * (its prefill writes one 2048-token chunk of one sequence): for the batched varlen prefill of
+ * the paged engine, whose sequences start anywhere in the packed input -- tiles that begin at
+ * each sequence's first row let whole page blocks take the 16-byte stores instead of bytes.
+ */
+int sdv_quant_append_tiles(const void* v_new, const void* k_new, const int32_t* slot_mapping,
+                           int32_t n_tokens, int32_t kv_heads, int32_t head_dim, int32_t group_size,
+                           int32_t num_layers, int64_t in_layer_stride,
+                           void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
+                           int64_t k_layer_stride, int64_t v_layer_stride, int64_t s_layer_stride,
+                           int32_t scale_mode, const int32_t* tile_starts, int32_t n_tiles, void* stream);
 
 /* Bytes of workspace sdv_paged_attention needs for these sizes (0 on invalid sizes). */
 size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q_heads,

@@ -7,8 +7,11 @@
 //
 // K is copied into the page's [D/8][16][8] chunk layout (see include/sdv.h).
 //
-// One wavefront handles 16 consecutive input tokens of one KV head of one layer; a
-// workgroup holds four such wavefronts (64 tokens).  D/8 lanes (a "row") hold one token's
+// One wavefront handles 16 consecutive input tokens of one KV head of one layer (or, with a
+// caller's tile table, the up-to-16 rows of one table entry: a batched varlen prefill passes
+// tiles that start where each sequence starts, so whole page blocks keep the 16-byte stores
+// although sequences start anywhere in the packed input); a workgroup holds four such
+// wavefronts.  D/8 lanes (a "row") hold one token's
 // head_dim values as 16-byte pieces, so each wave-wide load brings 64/(D/8) whole token rows
 // and a lane ends up holding J = 16 / rows consecutive tokens of the same 8 dimensions.  The
 // max-abs of a token is a DPP reduction inside its row (no cross-row traffic).  The V page
@@ -32,6 +35,8 @@ struct QuantArgs {
   const uint16_t* v_new;
   const uint16_t* k_new;
   const int32_t* slots;
+  const int32_t* tiles;  // optional tile table: tile i = rows [tiles[i], min(tiles[i] + 16, tiles[i+1]))
+  int n_tiles;
   int n_tokens;
   int kv_heads;
   int num_blocks;
@@ -76,7 +81,7 @@ __device__ __forceinline__ float quotient_rn(float x, float s, float r) {
   return copysignf(__builtin_fmaf(e, r, q0), x);
 }
 
-template <int D, bool WITH_K>
+template <int D, bool WITH_K, bool TABLE>
 __global__ __launch_bounds__(64 * kQuantWaves) void quant_append_kernel(QuantArgs a) {
   constexpr int LPR = D / 8;          // lanes per token row: 16 bytes of BF16 each
   constexpr int RPW = kWave / LPR;    // token rows per wave-wide load (4 or 8)
@@ -87,11 +92,20 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quant_append_kernel(QuantArg
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int r = lane / LPR, p = lane % LPR;
-  const int t0 = (blockIdx.x * kQuantWaves + wave) * kBlock;
-  if (t0 >= a.n_tokens) return;  // wave-uniform
+  const int tile = blockIdx.x * kQuantWaves + wave;
+  int t0, nt;
+  if constexpr (TABLE) {  // rows from the caller's table, clamped to the input
+    if (tile >= a.n_tiles) return;  // wave-uniform
+    t0 = min(max(a.tiles[tile], 0), a.n_tokens);
+    nt = min(min(a.tiles[tile + 1], a.n_tokens) - t0, kBlock);
+    if (nt <= 0) return;
+  } else {  // 16 consecutive rows
+    t0 = tile * kBlock;
+    if (t0 >= a.n_tokens) return;  // wave-uniform
+    nt = min(kBlock, a.n_tokens - t0);
+  }
   const int kvh = blockIdx.y;
   const int layer = blockIdx.z;
-  const int nt = min(kBlock, a.n_tokens - t0);
   const int KV = a.kv_heads;
 
   const uint16_t* vin = a.v_new + layer * a.in_ls;
@@ -235,12 +249,12 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quant_append_kernel(QuantArg
 
 using namespace sdv;
 
-extern "C" int sdv_quant_append(const void* v_new, const void* k_new, const int32_t* slot_mapping,
-                                int32_t n_tokens, int32_t kv_heads, int32_t head_dim,
-                                int32_t group_size, int32_t num_layers, int64_t in_layer_stride,
-                                void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
-                                int64_t k_layer_stride, int64_t v_layer_stride,
-                                int64_t s_layer_stride, int32_t scale_mode, void* stream) {
+static int quant_append(const void* v_new, const void* k_new, const int32_t* slot_mapping, int32_t n_tokens,
+                        int32_t kv_heads, int32_t head_dim, int32_t group_size, int32_t num_layers,
+                        int64_t in_layer_stride, void* k_pages, void* v_pages, float* v_scales,
+                        int32_t num_blocks, int64_t k_layer_stride, int64_t v_layer_stride,
+                        int64_t s_layer_stride, int32_t scale_mode, const int32_t* tiles, int32_t n_tiles,
+                        void* stream) {
   if (!v_new || !slot_mapping || !v_pages || !v_scales) return SDV_ERR_NULL;
   if (k_new && !k_pages) return SDV_ERR_NULL;
   if (n_tokens < 0 || kv_heads <= 0 || num_layers <= 0 || num_blocks <= 0) return SDV_ERR_SHAPE;
@@ -279,17 +293,58 @@ extern "C" int sdv_quant_append(const void* v_new, const void* k_new, const int3
   a.v_ls = num_layers > 1 ? v_layer_stride : 0;
   a.s_ls = num_layers > 1 ? s_layer_stride : 0;
 
-  const int tiles = (n_tokens + kBlock - 1) / kBlock;
-  dim3 grid((tiles + kQuantWaves - 1) / kQuantWaves, kv_heads, num_layers);
+  a.tiles = tiles;
+  a.n_tiles = n_tiles;
+
+  const int64_t n_waves = tiles ? n_tiles : (n_tokens + kBlock - 1) / kBlock;
+  if (n_waves == 0) return SDV_OK;
+  dim3 grid((unsigned)((n_waves + kQuantWaves - 1) / kQuantWaves), kv_heads, num_layers);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 block(64 * kQuantWaves);
-  if (head_dim == 128 && k_new)
-    hipLaunchKernelGGL((quant_append_kernel<128, true>), grid, block, 0, st, a);
-  else if (head_dim == 128)
-    hipLaunchKernelGGL((quant_append_kernel<128, false>), grid, block, 0, st, a);
-  else if (k_new)
-    hipLaunchKernelGGL((quant_append_kernel<64, true>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((quant_append_kernel<64, false>), grid, block, 0, st, a);
+  if (tiles) {
+    if (head_dim == 128 && k_new)
+      hipLaunchKernelGGL((quant_append_kernel<128, true, true>), grid, block, 0, st, a);
+    else if (head_dim == 128)
+      hipLaunchKernelGGL((quant_append_kernel<128, false, true>), grid, block, 0, st, a);
+    else if (k_new)
+      hipLaunchKernelGGL((quant_append_kernel<64, true, true>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((quant_append_kernel<64, false, true>), grid, block, 0, st, a);
+  } else {
+    if (head_dim == 128 && k_new)
+      hipLaunchKernelGGL((quant_append_kernel<128, true, false>), grid, block, 0, st, a);
+    else if (head_dim == 128)
+      hipLaunchKernelGGL((quant_append_kernel<128, false, false>), grid, block, 0, st, a);
+    else if (k_new)
+      hipLaunchKernelGGL((quant_append_kernel<64, true, false>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((quant_append_kernel<64, false, false>), grid, block, 0, st, a);
+  }
   return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
+}
+
+extern "C" int sdv_quant_append(const void* v_new, const void* k_new, const int32_t* slot_mapping,
+                                int32_t n_tokens, int32_t kv_heads, int32_t head_dim,
+                                int32_t group_size, int32_t num_layers, int64_t in_layer_stride,
+                                void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
+                                int64_t k_layer_stride, int64_t v_layer_stride,
+                                int64_t s_layer_stride, int32_t scale_mode, void* stream) {
+  return quant_append(v_new, k_new, slot_mapping, n_tokens, kv_heads, head_dim, group_size, num_layers,
+                      in_layer_stride, k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride,
+                      s_layer_stride, scale_mode, nullptr, 0, stream);
+}
+
+extern "C" int sdv_quant_append_tiles(const void* v_new, const void* k_new, const int32_t* slot_mapping,
+                                      int32_t n_tokens, int32_t kv_heads, int32_t head_dim,
+                                      int32_t group_size, int32_t num_layers, int64_t in_layer_stride,
+                                      void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
+                                      int64_t k_layer_stride, int64_t v_layer_stride,
+                                      int64_t s_layer_stride, int32_t scale_mode, const int32_t* tile_starts,
+                                      int32_t n_tiles, void* stream) {
+  if (!tile_starts) return SDV_ERR_NULL;
+  if (n_tiles < 0) return SDV_ERR_SHAPE;
+  if (!aligned(tile_starts, 4)) return SDV_ERR_ALIGN;
+  return quant_append(v_new, k_new, slot_mapping, n_tokens, kv_heads, head_dim, group_size, num_layers,
+                      in_layer_stride, k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride,
+                      s_layer_stride, scale_mode, tile_starts, n_tiles, stream);
 }

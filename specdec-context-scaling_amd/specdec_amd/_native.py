@@ -45,6 +45,8 @@ _SZ = ctypes.c_size_t
 SIGNATURES = {
     "sdv_quant_append": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I64,
                                         _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _P]),
+    "sdv_quant_append_tiles": (ctypes.c_int, [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I64,
+                                              _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _P, _I32, _P]),
     "sdv_attention_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "sdv_attention_workspace_init": (ctypes.c_int, [_P, _SZ, _P]),
     "sdv_attention_single_launch": (ctypes.c_int32, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),

@@ -79,6 +79,7 @@ class PagedKVCache:
         self.blocks: list[list[int]] = [[] for _ in range(batch)]
         self.lengths: list[int] = [0] * batch
         self._bt = None
+        self._tiles = None  # (lengths, device tile table) of the last prefill
 
     # ------------------------------------------------------------------ storage
     def _new_pages(self, nb: int):
@@ -178,6 +179,8 @@ class PagedKVCache:
 
         k_new/v_new BF16 (sum(lengths), KV, D), sequence after sequence (the varlen layout);
         lengths become ``lengths``.  Returns the slot mapping so that later layers can pass it.
+        The launch takes a tile table that starts a tile at every sequence's first row (built
+        once per set of lengths), so whole page blocks are written with 16-byte stores.
         """
         if len(lengths) != self.batch:
             raise ValueError(f"{len(lengths)} lengths for a batch of {self.batch}")
@@ -185,8 +188,13 @@ class PagedKVCache:
             self.reserve(b, n)
         if slots is None:
             slots = self.varlen_slots(lengths)
+        key = tuple(lengths)
+        if self._tiles is None or self._tiles[0] != key:
+            t = torch.tensor(ops.varlen_tile_starts(list(lengths)), dtype=torch.int32).to(self.device)
+            self._tiles = (key, t)
         kp, vp, vs = self.layer(layer)
-        ops.quant_append(v_new, slots, kp, vp, vs, k_new, scale_mode=self.scale_mode)
+        ops.quant_append(v_new, slots, kp, vp, vs, k_new, scale_mode=self.scale_mode,
+                         tile_starts=self._tiles[1])
         for b, n in enumerate(lengths):
             self.lengths[b] = n
         return slots

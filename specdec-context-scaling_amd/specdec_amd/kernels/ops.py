@@ -139,13 +139,15 @@ def attention_workspace_bytes(num_layers: int, batch: int, q_heads: int, kv_head
 
 def quant_append(v_new: torch.Tensor, slot_mapping: torch.Tensor, k_pages: torch.Tensor,
                  v_pages: torch.Tensor, v_scales: torch.Tensor, k_new: torch.Tensor | None = None,
-                 *, scale_mode: str = "div") -> None:
+                 *, scale_mode: str = "div", tile_starts: torch.Tensor | None = None) -> None:
     """Quantize V to FP8 and write V (and BF16 K when given) into page slots, in place.
 
     v_new/k_new: BF16 (n_tokens, KV, D), or (L, n_tokens, KV, D) with layered pages.
     slot_mapping: int32 (n_tokens,), slot = block * 16 + offset, negative = skip.
     Pages: k (…, num_blocks, KV, D/8, 16, 8) BF16; v (…, num_blocks, KV, D, 16) uint8 or
     float8_e4m3fn; scales (…, num_blocks, KV, 16) fp32.
+    tile_starts: optional int32 (n_tiles + 1,) on the device: tile i is rows
+    [tile_starts[i], min(tile_starts[i] + 16, tile_starts[i+1])) (see varlen_tile_starts).
     """
     lib = _native.load()
     _need(v_new, "v_new", (torch.bfloat16,), ndim=(3, 4))
@@ -175,11 +177,41 @@ def quant_append(v_new: torch.Tensor, slot_mapping: torch.Tensor, k_pages: torch
     if k_new is not None and k_new.data_ptr() % 16:
         k_new = k_new.clone()
     per = lambda t: t[0].numel() if layered else 0  # noqa: E731  (elements per layer)
-    st = lib.sdv_quant_append(_p(v_new), _p(k_new), _p(slot_mapping), n_tokens, kv, d, d, L,
-                              per(v_new), _p(k_pages), _p(v_pages), _p(v_scales), nb,
-                              per(k_pages), per(v_pages), per(v_scales), _SCALE_MODES[scale_mode],
-                              _stream(dev))
-    _native.check(st, "sdv_quant_append")
+    if tile_starts is None:
+        st = lib.sdv_quant_append(_p(v_new), _p(k_new), _p(slot_mapping), n_tokens, kv, d, d, L,
+                                  per(v_new), _p(k_pages), _p(v_pages), _p(v_scales), nb,
+                                  per(k_pages), per(v_pages), per(v_scales), _SCALE_MODES[scale_mode],
+                                  _stream(dev))
+        _native.check(st, "sdv_quant_append")
+        return
+    _need(tile_starts, "tile_starts", (torch.int32,), dev, ndim=(1,))
+    if tile_starts.shape[0] < 1:
+        _fail("tile_starts needs n_tiles + 1 entries")
+    st = lib.sdv_quant_append_tiles(_p(v_new), _p(k_new), _p(slot_mapping), n_tokens, kv, d, d, L,
+                                    per(v_new), _p(k_pages), _p(v_pages), _p(v_scales), nb,
+                                    per(k_pages), per(v_pages), per(v_scales), _SCALE_MODES[scale_mode],
+                                    _p(tile_starts), tile_starts.shape[0] - 1, _stream(dev))
+    _native.check(st, "sdv_quant_append_tiles")
+
+
+def varlen_tile_starts(lengths: list[int], starts: list[int] | None = None) -> list[int]:
+    """Tile table for a packed varlen input of sequences with `lengths` tokens whose first token
+    lands at position `starts[b]` of its sequence (0: a whole prompt): tiles break where a page
+    block begins, so every whole block is one tile.  n_tiles + 1 entries; the last is the
+    total row count."""
+    starts = starts or [0] * len(lengths)
+    out, row = [], 0
+    for n, p0 in zip(lengths, starts):
+        if n < 0 or p0 < 0:
+            raise ValueError("negative length or start position")
+        i = 0
+        while i < n:
+            step = min(n - i, 16 - (p0 + i) % 16)
+            out.append(row + i)
+            i += step
+        row += n
+    out.append(row)
+    return out
 
 
 def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, v_scales: torch.Tensor,

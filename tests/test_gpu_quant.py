@@ -176,3 +176,45 @@ def test_prefill_mixed_tiles(cuda_device, d):
     assert np.array_equal(vp[0].cpu().numpy(), ev)
     assert np.array_equal(vs[0].cpu().numpy().view(np.uint32), es.view(np.uint32))
     assert np.array_equal(bits16(kp[0]), ek)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_varlen_prefill_tile_table(cuda_device, d):
+    """A packed varlen prefill through sdv_quant_append_tiles: sequences of ragged lengths
+    whose first tokens land at various positions of their first page block (a whole prompt,
+    or an append to a partly filled block), an empty sequence, fragmented pages.  Bytes and
+    scales bit-exact against the oracle, and equal to the launch without a table."""
+    announce(f"quant varlen prefill tile table d={d}")
+    lengths = [37, 16, 5, 0, 100, 33, 700]
+    starts = [0, 0, 3, 0, 15, 16, 9]
+    kv, nb = 2, 128
+    perm = np.random.default_rng(5).permutation(nb)
+    parts, at = [], 0
+    for n, p0 in zip(lengths, starts):
+        need = (p0 + n + 15) // 16
+        blocks = perm[at:at + need]
+        at += need
+        pos = np.arange(p0, p0 + n)
+        parts.append(blocks[pos // 16] * 16 + pos % 16)
+    slots = np.concatenate(parts).astype(np.int32)
+    n = len(slots)
+    g = wl.gen(91 + d)
+    v = wl.randn_bf16((n, kv, d), g)
+    k = wl.randn_bf16((n, kv, d), g)
+    tiles = torch.tensor(ops.varlen_tile_starts(lengths, starts), dtype=torch.int32, device=cuda_device)
+    kp, vp, vs = _pages(cuda_device, 1, nb, kv, d)
+    ops.quant_append(v.to(cuda_device), to_dev(slots, cuda_device), kp[0], vp[0], vs[0], k.to(cuda_device),
+                     tile_starts=tiles)
+    kp2, vp2, vs2 = _pages(cuda_device, 1, nb, kv, d)
+    ops.quant_append(v.to(cuda_device), to_dev(slots, cuda_device), kp2[0], vp2[0], vs2[0], k.to(cuda_device))
+    torch.cuda.synchronize()
+    q, s = quantize_rows(v)
+    ek, ev, es = opaged.alloc(nb, kv, d)
+    ev[:] = 0xA5
+    es[:] = -7.0
+    opaged.write(ek, ev, es, bits16(k), q, s, slots)
+    assert np.array_equal(vp[0].cpu().numpy(), ev)
+    assert np.array_equal(vs[0].cpu().numpy().view(np.uint32), es.view(np.uint32))
+    assert np.array_equal(bits16(kp[0]), ek)
+    assert torch.equal(vp, vp2) and torch.equal(vs.view(torch.int32), vs2.view(torch.int32))
+    assert torch.equal(kp.view(torch.int16), kp2.view(torch.int16))

@@ -89,6 +89,23 @@ def test_quant_host_validation(lib):
     assert _quant(lib, n=0) == _native.SDV_OK                  # nothing to do, no launch
 
 
+def test_quant_tiles_host_validation(lib):
+    def q(**kw):
+        a = dict(v=P, k=N, sl=P, n=16, KV=2, D=128, gs=128, L=1, ils=0, kp=P, vp=P, vs=P, nb=8, kls=0, vls=0,
+                 sls=0, mode=0, t=P, nt=1, st=N)
+        a.update(kw)
+        return lib.sdv_quant_append_tiles(a["v"], a["k"], a["sl"], a["n"], a["KV"], a["D"], a["gs"], a["L"],
+                                          a["ils"], a["kp"], a["vp"], a["vs"], a["nb"], a["kls"], a["vls"],
+                                          a["sls"], a["mode"], a["t"], a["nt"], a["st"])
+    assert q(t=N) == _native.SDV_ERR_NULL
+    assert q(nt=-1) == _native.SDV_ERR_SHAPE
+    assert q(t=ctypes.c_void_p(0x1002)) == _native.SDV_ERR_ALIGN
+    assert q(v=N) == _native.SDV_ERR_NULL                       # the checks of sdv_quant_append apply
+    assert q(gs=32) == _native.SDV_ERR_UNSUPPORTED
+    assert q(nt=0) == _native.SDV_OK                            # no tiles: nothing to do, no launch
+    assert q(n=0) == _native.SDV_OK
+
+
 def test_workspace_size_is_pure_host(lib):
     a = lib.sdv_attention_workspace_size(1, 1, 12, 2, 1, 128, 8192)
     b = lib.sdv_attention_workspace_size(28, 1, 12, 2, 1, 128, 8192)

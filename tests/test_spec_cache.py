@@ -130,3 +130,33 @@ def test_block_allocator_seeded_fragmentation():
         b.alloc(65)
     b.grow(80)
     assert len(b.alloc(70)) == 70
+
+
+def test_varlen_tile_starts_cover_rows_and_follow_blocks():
+    """The prefill tile table covers every packed row exactly once, never crosses a page block,
+    and makes every whole page block one tile (so the kernel takes its 16-byte stores)."""
+    import random
+    from specdec_amd.kernels import ops
+    rng = random.Random(11)
+    for _ in range(200):
+        nseq = rng.randint(1, 6)
+        lengths = [rng.choice([0, 1, 5, 15, 16, 17, 31, 32, 33, rng.randint(0, 200)]) for _ in range(nseq)]
+        starts = [rng.choice([0, 0, 3, 15, 16, rng.randint(0, 100)]) for _ in range(nseq)]
+        t = ops.varlen_tile_starts(lengths, starts)
+        assert t[-1] == sum(lengths) and t == sorted(t)
+        assert all(0 < b - a <= 16 for a, b in zip(t, t[1:]))
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        tiles = set(zip(t, t[1:]))
+        for b, (n, p0) in enumerate(zip(lengths, starts)):
+            for a_, e in tiles:
+                if cu[b] <= a_ < cu[b + 1]:
+                    assert e <= cu[b + 1]                                 # no tile spans two sequences
+                    first, last = p0 + a_ - cu[b], p0 + e - 1 - cu[b]
+                    assert first // 16 == last // 16                      # one page block per tile
+            for blk in range((p0 + 15) // 16, (p0 + n) // 16):            # whole blocks inside the run
+                a_ = cu[b] + 16 * blk - p0
+                assert (a_, a_ + 16) in tiles
+    with pytest.raises(ValueError):
+        ops.varlen_tile_starts([-1])

@@ -869,23 +869,29 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   float* lparts = reinterpret_cast<float*>(smem + lay.parts);
   float2* lgs = reinterpret_cast<float2*>(smem + lay.gstats);  // per row: group (max, 1/sum)
   // the group's statistics: wavefront 0 waits until all nvq items have published, merges them
-  // in a fixed order -- lane group g takes items g, g+4, ..., then the xor tree -- and shares
+  // in a fixed order -- item slice j takes items j, j+nsl, ..., then a fixed tree -- and shares
   // (max, 1/sum) of each row through LDS, so every wavefront and workgroup of the group gets
   // identical values.  The other wavefronts' V loads stay in flight across the barrier.
   auto group_stats = [&](float (&gm)[NT], float (&ginv)[NT]) {
     if (wave == 0) {
       constexpr int PB = D == 128 ? 16 : 8;  // entries in flight per lane (registers allow)
-      const int ne = (nvq - g + 3) >> 2;     // items of this lane group (<= 16)
-      const int ne_max = (nvq + 3) >> 2;  // wave-uniform loop bound
+      // lane = (item slice, row): 16 rows x 4 slices, or 8 x 8 when the rows fit in 8 and the
+      // group has more than 8 items, so that more lanes share the merges (one layer at 8K, 64
+      // items: 13.3 -> 12.8 us; with 4 or 5 items the extra tree level costs more than it saves)
+      const bool narrow = NT == 1 && a.R <= 8 && nvq > 8;
+      const int nsl = narrow ? 8 : 4;                      // item slices
+      const int rl = narrow ? (lane & 7) : n, sl = narrow ? (lane >> 3) : g;
+      const int ne = (nvq - sl + nsl - 1) / nsl;           // items of this slice (<= PB)
+      const int ne_max = (nvq + nsl - 1) / nsl;            // wave-uniform loop bound
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const int rr = nt * 16 + n;
+        const int rr = nt * 16 + rl;
         const float2* fp = fs + (int64_t)item0 * 64 + (rr < a.R ? rr : 0);
         float m = -INFINITY, l = 0.0f;
         for (int k0 = 0; k0 < ne_max; k0 += PB) {
           uint64_t e[PB];
 #pragma unroll
-          for (int k = 0; k < PB; ++k) e[k] = k0 + k < ne ? load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64) : 1;
+          for (int k = 0; k < PB; ++k) e[k] = k0 + k < ne ? load_dev_u64(fp + (int64_t)(sl + nsl * (k0 + k)) * 64) : 1;
           unsigned spins = 0;
           for (;;) {
             bool ready = true;
@@ -899,7 +905,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
             for (int k = 0; k < PB; ++k)
-              if (e[k] == 0) e[k] = load_dev_u64(fp + (int64_t)(g + 4 * (k0 + k)) * 64);
+              if (e[k] == 0) e[k] = load_dev_u64(fp + (int64_t)(sl + nsl * (k0 + k)) * 64);
           }
 #pragma unroll
           for (int k = 0; k < PB; ++k) {
@@ -909,9 +915,10 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
             }
           }
         }
+        if (narrow) merge_xor_low<8>(m, l);  // slices 2j and 2j+1 (lanes with bit 3 clear)
         merge_lanes<16>(m, l);
         merge_lanes<32>(m, l);
-        if (g == 0 && rr < a.R) lgs[rr] = make_float2(m, 1.0f / l);
+        if (sl == 0 && rr < a.R) lgs[rr] = make_float2(m, 1.0f / l);
       }
     }
     __syncthreads();

@@ -575,6 +575,14 @@ constexpr int kFusedMaxChunks = 64;     // items per group
 #define SDV_FUSED_MIN_BLOCKS 1
 #endif
 constexpr int kFusedMinBlocks = SDV_FUSED_MIN_BLOCKS;
+// Most items per group.  A one-layer call is split as finely as this allows; 32 items (4
+// blocks each at T=2048, 16 at 8K) beat 64 (10.2-10.5 vs 10.9 us at 2K; 28 per-layer calls in
+// a graph 13.0 vs 13.4 us per layer at 8K): fewer entries to merge and sum per group.
+#ifndef SDV_FUSED_GROUP_ITEMS  // tuning builds: other caps
+#define SDV_FUSED_GROUP_ITEMS 32
+#endif
+constexpr int kFusedGroupItems = SDV_FUSED_GROUP_ITEMS;
+static_assert(kFusedGroupItems <= kFusedMaxChunks, "the output stage holds kFusedMaxChunks items");
 #ifndef SDV_FUSED_MAX_PER_CU  // tuning builds: resident decode workgroups per CU
 #define SDV_FUSED_MAX_PER_CU 1
 #endif
@@ -1431,9 +1439,9 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
   if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;
   const int G = (int)p.groups;
   const int gb = (max_seq_len + kBlock - 1) / kBlock;
-  // items of at least kFusedMinBlocks blocks: a small problem (one layer) spread over every CU
-  // would spend its time in the cross-workgroup exchanges, not in streaming
-  const int max_items = min(min(kFusedMaxChunks, gb), max(1, gb / kFusedMinBlocks));
+  // at most kFusedGroupItems items of at least kFusedMinBlocks blocks: a small problem (one
+  // layer) spread over every CU would spend its time in the cross-workgroup exchanges
+  const int max_items = min(min(kFusedGroupItems, gb), max(1, gb / kFusedMinBlocks));
   // items whose fp32 partials fit the sync area
   const int part_cap = (int)(kSyncPartBytes / ((size_t)R * D * 4));
   int cap = min(part_cap, fused_capacity<D, NT, W>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total));

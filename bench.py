@@ -342,8 +342,12 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
         row["five_decodes_us"] = round(5 * row["per_layer_calls_us_per_layer"] * dL, 1)
     _progress("cfg3 chains")
     out["cfg3_draft_chain_5x24_T8192"] = chain_row(torch, dev, dreps, dL, dH, dKV, dD, 8192, 1, 5)
+    out["cfg3_draft_chain_5x24_T8192_fused"] = chain_row(torch, dev, dreps, dL, dH, dKV, dD, 8192, 1, 5,
+                                                         fused=True)
     del dreps
     out["cfg3_target_verify_step_28_T8192"] = chain_row(torch, dev, reps8k, L, H, KV, D, 8192, 5, 1)
+    out["cfg3_target_verify_step_28_T8192_fused"] = chain_row(torch, dev, reps8k, L, H, KV, D, 8192, 5, 1,
+                                                              fused=True)
     # config 4: B=32 ragged contexts U{2048..32768}, fragmented pool, 1% outlier channels x20
     lens = wl.ragged_lengths(32, 2048, 32768, seed=41)
     creps = _build(torch, dev, L, KV, D, lens, 1, seed0=4000, outliers=True)
@@ -381,11 +385,12 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
     return out
 
 
-def chain_row(torch, dev, reps, layers, h, kv, d, T, s, steps):
+def chain_row(torch, dev, reps, layers, h, kv, d, T, s, steps, fused=False):
     """The engine's per-layer call pattern for `steps` speculative steps, in one HIP graph: per
     step and layer, kernel 1 appends the step's s new tokens (BF16 K copy and FP8 V) at the end
     of the context, then the layer's attention runs over it (T tokens after the last step).
-    Draft chain: s=1, 5 steps; target verify: s=5, 1 step."""
+    Draft chain: s=1, 5 steps; target verify: s=5, 1 step.  fused: both in one
+    sdv_paged_attention_append call per layer (the single launch writes the new tokens)."""
     from specdec_amd import workloads as wl
     from specdec_amd.kernels import ops
 
@@ -409,13 +414,17 @@ def chain_row(torch, dev, reps, layers, h, kv, d, T, s, steps):
         for j in range(steps):
             for layer in range(layers):
                 kp, vp, vs = c.layer(layer)
+                if fused:
+                    ops.paged_attention(q[j, layer], kp, vp, vs, bt, lens[j], T, out=out, workspace_tensor=ws,
+                                        append=(k_new[j, layer], v_new[j, layer], slots[j]))
+                    continue
                 ops.quant_append(v_new[j, layer], slots[j], kp, vp, vs, k_new[j, layer])
                 ops.paged_attention(q[j, layer], kp, vp, vs, bt, lens[j], T, out=out, workspace_tensor=ws)
 
     # the graph-capture helper replays several chains per graph; keep the graph small
     us = _time_chain(torch, chain, len(reps))
     nbytes = steps * layers * (wl.bytes_attn(T, s, h, kv, d) + wl.bytes_quant_append(s, kv, d, True))
-    return {"layers": layers, "steps": steps, "q_len": s, "T": T, "launches": 2 * steps * layers,
+    return {"layers": layers, "steps": steps, "q_len": s, "T": T, "launches": (1 if fused else 2) * steps * layers,
             "us_per_chain": round(us, 1), "us_per_layer_step": round(us / (steps * layers), 3),
             "GBps": _gbs(nbytes, us)}
 

@@ -29,6 +29,8 @@
  *                           -> pybind attention (specdec/kernels/cuda/bind.cpp:16)
  *                           -> attention_cuda (specdec/kernels/cuda/attention.cu:244-288)
  *                           computes, with FP8 V dequantized inside the kernel
+ *   sdv_paged_attention_append <- no counterpart: sdv_quant_append + sdv_paged_attention
+ *                           in one call (the single launch writes the new tokens itself)
  *   sdv_quant_append_tiles <- no counterpart: sdv_quant_append for the engine's batched
  *                           varlen prefill (a table of 16-row tiles that follow each
  *                           sequence's start)
@@ -173,6 +175,31 @@ int sdv_paged_attention_phases(const void* q, const void* k_pages, const void* v
                                int32_t q_len, int32_t head_dim, int32_t max_seq_len,
                                int32_t q_token_major, void* workspace, size_t workspace_bytes,
                                void* out, void* stream, int32_t phase_mask);
+
+/*
+ * sdv_quant_append of the q_len new tokens of every sequence followed by sdv_paged_attention
+ * over the context that includes them, in one call: the same bytes in the pages and the same
+ * output as the two calls in that order.  k_new/v_new: bf16 [num_layers][batch*q_len][kv_heads]
+ * [head_dim] (layers new_layer_stride elements apart), token b*q_len + i at position
+ * seq_lens[b] - q_len + i, slot_mapping int32 [batch*q_len] (negative = skip), scale_mode as
+ * for sdv_quant_append.  On the single-launch path each workgroup writes the new tokens that
+ * fall in its own page blocks before reading them, so the append costs no launch of its own;
+ * otherwise the append kernel runs first on the same stream.  No counterpart in the reference:
+ * its layer forward quantizes and concatenates V (model_self.py:697-706, 778-800) and then
+ * attends (model_self.py:739-776) as separate steps; this is both, for the engine's per-layer
+ * decode and verify calls.
+ */
+int sdv_paged_attention_append(const void* q, const void* k_pages, const void* v_pages,
+                               const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                               int64_t v_layer_stride, int64_t s_layer_stride,
+                               const int32_t* block_table, int32_t max_blocks_per_seq,
+                               const int32_t* seq_lens,
+                               int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                               int32_t q_len, int32_t head_dim, int32_t max_seq_len,
+                               int32_t q_token_major, void* workspace, size_t workspace_bytes,
+                               void* out, const void* k_new, const void* v_new,
+                               const int32_t* slot_mapping, int64_t new_layer_stride,
+                               int32_t scale_mode, void* stream);
 
 /* Elementwise fp32 -> E4M3FN (RNE, NaN beyond 464 / for Inf and NaN), device buffers. */
 int sdv_fp8_encode(const float* in, uint8_t* out, int64_t n, void* stream);

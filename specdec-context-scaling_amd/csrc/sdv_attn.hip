@@ -59,6 +59,14 @@ struct AttnArgs {
   int pv_bpw, pv_chunk_tokens, n_pv_chunks;
   int score_stride;
   float inv_sqrt_d;
+  // in-kernel append (sdv_paged_attention_append, single launch): the S new tokens of every
+  // sequence, BF16 [L][B*S][KV][D] (layers app_ls elements apart), token b*S + i at position
+  // seq_len - S + i; app_v == nullptr: no append
+  const uint16_t* app_k;
+  const uint16_t* app_v;
+  const int32_t* app_slots;
+  int64_t app_ls;
+  int app_scale_mode;
 };
 
 __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
@@ -537,6 +545,56 @@ __global__ __launch_bounds__(256) void reduce_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------- in-kernel append
+// The new tokens of one (layer, sequence, KV head) whose positions fall in page blocks
+// [blk_lo, blk_hi) of the sequence, written into the pages exactly as sdv_quant_append writes
+// them (scale per token and KV head, E4M3FN codes, BF16 K copy; the same helpers): wavefront w
+// takes positions w, w + W, ...; lanes p < D/8 hold dimensions 8p .. 8p+7 of the token.
+template <int D, int W>
+__device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, int b, int kvh, int T, int blk_lo,
+                                                  int blk_hi, int wave, int lane) {
+  constexpr int LPR = D / 8;
+  const int first = T - a.S;  // position of new token 0
+  const int p_lo = max(max(first, blk_lo * kBlock), 0), p_hi = min(T, blk_hi * kBlock);
+  const int64_t n_slots = (int64_t)a.num_blocks * kBlock;
+  const int p = lane < LPR ? lane : 0;
+  uint16_t* kp = const_cast<uint16_t*>(a.k_pages) + layer * a.k_ls;
+  uint8_t* vp = const_cast<uint8_t*>(a.v_pages) + layer * a.v_ls;
+  float* sp = const_cast<float*>(a.v_scales) + layer * a.s_ls;
+  for (int pos = p_lo + wave; pos < p_hi; pos += W) {  // wave-uniform
+    const int row = b * a.S + (pos - first);
+    const int slot = a.app_slots[row];
+    if (slot < 0 || (int64_t)slot >= n_slots) continue;
+    const int64_t in = layer * a.app_ls + ((int64_t)row * a.KV + kvh) * D + 8 * p;
+    const uint4 vw = *reinterpret_cast<const uint4*>(a.app_v + in);
+    const uint4 kw = *reinterpret_cast<const uint4*>(a.app_k + in);
+    float sc, rcp;
+    bool fast;
+    token_scale(row_max_bits<LPR>(abs_max_bits8(vw)), a.app_scale_mode, sc, rcp, fast);
+    const int blk = slot >> 4, off = slot & (kBlock - 1);
+    const int64_t page = (int64_t)blk * a.KV + kvh;
+    if (lane < LPR) {
+      const uint32_t w[4] = {vw.x, vw.y, vw.z, vw.w};
+      uint8_t* vrow = vp + (page * D + 8 * p) * kBlock + off;
+#pragma unroll
+      for (int k = 0; k < 8; k += 2) {
+        const float x0 = __uint_as_float(w[k >> 1] << 16), x1 = __uint_as_float(w[k >> 1] & 0xFFFF0000u);
+        uint32_t c2;
+        if (fast) {
+          c2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(quotient_rn(x0, sc, rcp), quotient_rn(x1, sc, rcp), 0,
+                                                          false);
+        } else {  // max-abs not finite or in (0, 2^-60): exact division and the integer encoder
+          c2 = e4m3fn_encode(x0 / sc) | (e4m3fn_encode(x1 / sc) << 8);
+        }
+        vrow[k * kBlock] = (uint8_t)c2;
+        vrow[(k + 1) * kBlock] = (uint8_t)(c2 >> 8);
+      }
+      *reinterpret_cast<uint4*>(kp + page * kBlock * D + (p * kBlock + off) * 8) = kw;
+      if (lane == 0) sp[page * kBlock + off] = sc;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------- fused
 // One launch for the shapes whose whole grid fits the device at once (one query-row group:
 // decode and verify).  One workgroup per CU (W = 8 or 16 wavefronts for decode; 8 or 4 when
@@ -728,6 +786,13 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
   }
   if (tid == 0) s_next = s_next2 = 0;
+  // the group's new tokens inside this item's blocks go into the pages first; the barrier
+  // (workgroup-scope release and acquire) makes them visible to the loads below, and only
+  // this workgroup reads these blocks
+  if (a.app_v) {
+    append_new_tokens<D, W>(a, layer, b, kvh, T, blk_lo, blk_lo + nbk, wave, lane);
+    __threadfence_block();
+  }
   __syncthreads();
 
   // ------------------------------------------------------------------ 1. q.k^T
@@ -1545,14 +1610,21 @@ extern "C" size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch
   return p.total;
 }
 
-extern "C" int sdv_paged_attention_phases(const void* q, const void* k_pages, const void* v_pages,
-                                          const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
-                                          int64_t v_layer_stride, int64_t s_layer_stride,
-                                          const int32_t* block_table, int32_t max_blocks_per_seq,
-                                          const int32_t* seq_lens, int32_t num_layers, int32_t batch,
-                                          int32_t q_heads, int32_t kv_heads, int32_t q_len, int32_t head_dim,
-                                          int32_t max_seq_len, int32_t q_token_major, void* workspace,
-                                          size_t workspace_bytes, void* out, void* stream, int32_t phase_mask) {
+// The new tokens to append before attending (sdv_paged_attention_append).
+struct AppendIn {
+  const void* k_new;
+  const void* v_new;
+  const int32_t* slot_mapping;
+  int64_t layer_stride;
+  int32_t scale_mode;
+};
+
+static int attention(const void* q, const void* k_pages, const void* v_pages, const float* v_scales,
+                     int32_t num_blocks, int64_t k_layer_stride, int64_t v_layer_stride, int64_t s_layer_stride,
+                     const int32_t* block_table, int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                     int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t q_len,
+                     int32_t head_dim, int32_t max_seq_len, int32_t q_token_major, void* workspace,
+                     size_t workspace_bytes, void* out, void* stream, int32_t phase_mask, const AppendIn* app) {
   if (phase_mask <= 0 || phase_mask > SDV_PHASE_ALL) return SDV_ERR_SHAPE;
   if (!q || !k_pages || !v_pages || !v_scales || !block_table || !seq_lens || !out) return SDV_ERR_NULL;
   if (head_dim != 64 && head_dim != 128) return SDV_ERR_UNSUPPORTED;
@@ -1619,13 +1691,74 @@ extern "C" int sdv_paged_attention_phases(const void* q, const void* k_pages, co
   // RN(1/sqrt(D)): 1/sqrt(128) = 0.08838834764831845, 1/sqrt(64) = 0.125 exactly
   a.inv_sqrt_d = head_dim == 128 ? 0.08838834764831845f : 0.125f;
 
+  a.app_k = a.app_v = nullptr;
+  a.app_slots = nullptr;
+  a.app_ls = 0;
+  a.app_scale_mode = 0;
+
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (app) {
+    const int64_t per_layer = (int64_t)batch * q_len * kv_heads * head_dim;
+    if (!app->k_new || !app->v_new || !app->slot_mapping) return SDV_ERR_NULL;
+    if (app->scale_mode != SDV_SCALE_DIV && app->scale_mode != SDV_SCALE_RCP) return SDV_ERR_UNSUPPORTED;
+    if (num_layers > 1 && app->layer_stride < per_layer) return SDV_ERR_SHAPE;
+    if (!aligned(app->k_new, 16) || !aligned(app->v_new, 16) || !aligned(app->slot_mapping, 4) ||
+        (num_layers > 1 && app->layer_stride % 8 != 0))
+      return SDV_ERR_ALIGN;
+    const int R = (q_heads / kv_heads) * q_len;
+    const bool fused = (head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len) : fused_grid_for<64>(p, R, max_seq_len)) > 0;
+    if (fused) {  // the single launch writes the new tokens itself
+      a.app_k = static_cast<const uint16_t*>(app->k_new);
+      a.app_v = static_cast<const uint16_t*>(app->v_new);
+      a.app_slots = app->slot_mapping;
+      a.app_ls = num_layers > 1 ? app->layer_stride : 0;
+      a.app_scale_mode = app->scale_mode;
+    } else {  // three launches: the append kernel first, on the same stream
+      const int st_app = sdv_quant_append(app->v_new, app->k_new, app->slot_mapping, batch * q_len, kv_heads,
+                                          head_dim, head_dim, num_layers, app->layer_stride,
+                                          const_cast<void*>(k_pages), const_cast<void*>(v_pages),
+                                          const_cast<float*>(v_scales), num_blocks, k_layer_stride,
+                                          v_layer_stride, s_layer_stride, app->scale_mode, stream);
+      if (st_app != SDV_OK) return st_app;
+    }
+  }
   const int zdim = num_layers * batch;
   if (head_dim == 128)
     launch_all<128>(a, p, zdim, st, phase_mask);
   else
     launch_all<64>(a, p, zdim, st, phase_mask);
   return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
+}
+
+extern "C" int sdv_paged_attention_phases(const void* q, const void* k_pages, const void* v_pages,
+                                          const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                                          int64_t v_layer_stride, int64_t s_layer_stride,
+                                          const int32_t* block_table, int32_t max_blocks_per_seq,
+                                          const int32_t* seq_lens, int32_t num_layers, int32_t batch,
+                                          int32_t q_heads, int32_t kv_heads, int32_t q_len, int32_t head_dim,
+                                          int32_t max_seq_len, int32_t q_token_major, void* workspace,
+                                          size_t workspace_bytes, void* out, void* stream, int32_t phase_mask) {
+  return attention(q, k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride, s_layer_stride,
+                   block_table, max_blocks_per_seq, seq_lens, num_layers, batch, q_heads, kv_heads, q_len,
+                   head_dim, max_seq_len, q_token_major, workspace, workspace_bytes, out, stream, phase_mask,
+                   nullptr);
+}
+
+extern "C" int sdv_paged_attention_append(const void* q, const void* k_pages, const void* v_pages,
+                                          const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                                          int64_t v_layer_stride, int64_t s_layer_stride,
+                                          const int32_t* block_table, int32_t max_blocks_per_seq,
+                                          const int32_t* seq_lens, int32_t num_layers, int32_t batch,
+                                          int32_t q_heads, int32_t kv_heads, int32_t q_len, int32_t head_dim,
+                                          int32_t max_seq_len, int32_t q_token_major, void* workspace,
+                                          size_t workspace_bytes, void* out, const void* k_new, const void* v_new,
+                                          const int32_t* slot_mapping, int64_t new_layer_stride,
+                                          int32_t scale_mode, void* stream) {
+  const AppendIn app{k_new, v_new, slot_mapping, new_layer_stride, scale_mode};
+  return attention(q, k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride, s_layer_stride,
+                   block_table, max_blocks_per_seq, seq_lens, num_layers, batch, q_heads, kv_heads, q_len,
+                   head_dim, max_seq_len, q_token_major, workspace, workspace_bytes, out, stream, SDV_PHASE_ALL,
+                   &app);
 }
 
 extern "C" int sdv_paged_attention(const void* q, const void* k_pages, const void* v_pages,

@@ -80,6 +80,64 @@ __device__ __forceinline__ float e4m3fn_decode(uint32_t w, int sel) {
   }
 }
 
+// ---------------------------------------------------------------- V quantization
+// Shared by the append kernel and the single launch's in-kernel append, so both write the
+// same bytes.
+
+// Max over the `LPR` lanes of each row (LPR = 8 or 16 consecutive lanes) of non-negative
+// fp32 bit patterns (unsigned compare; NaN propagates like torch.amax).  Every lane of the
+// row receives the row's maximum.
+template <int LPR>
+__device__ __forceinline__ uint32_t row_max_bits(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // half-row mirror
+  if (LPR == 16)
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row mirror
+  return v;
+}
+
+// Max-abs bit pattern of the 8 BF16 values of a 16-byte piece (sign cleared).
+__device__ __forceinline__ uint32_t abs_max_bits8(uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t mb = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    mb = max(mb, (w[i] << 16) & 0x7FFFFFFFu);
+    mb = max(mb, w[i] & 0x7FFF0000u);
+  }
+  return mb;
+}
+
+// Smallest max-abs (fp32 bits, 2^-60) of the fast route below: from there up to the largest
+// finite value, 1/s stays a normal fp32 and every intermediate that can change a code is normal.
+constexpr uint32_t kFastMinAmaxBits = 0x21800000u;
+
+// RN(x / s) from r = RN(1/s): q0 = RN(x r), e = x - s q0 (exact, one fma), RN(q0 + e r)
+// (Markstein's correction step).  For s = RN(max|v| / 448) or RN(max|v| * RN(1/448)) with
+// max|v| = 0 or in [2^-60, max finite], and every BF16 x with |x| <= max|v|, the E4M3FN code
+// of this value equals the code of the IEEE quotient: tests/native/quotient_check.c walks all
+// such (max|v|, x) pairs and finds no difference (fp32 results differ only below 2^-10, code 0).
+// The sign is copied from x, as the quotient by a positive s has it (also for -0).
+__device__ __forceinline__ float quotient_rn(float x, float s, float r) {
+#pragma clang fp contract(off)
+  const float ax = fabsf(x);
+  const float q0 = ax * r;
+  const float e = __builtin_fmaf(-q0, s, ax);
+  return copysignf(__builtin_fmaf(e, r, q0), x);
+}
+
+// Per token: s = max|v| / 448 evaluated per scale_mode (0: IEEE division, 1: times RN(1/448)),
+// s == 0 -> 1; r = RN(1/s); fast: whether quotient_rn's proof covers this max-abs (bits ab).
+__device__ __forceinline__ void token_scale(uint32_t ab, int scale_mode, float& s, float& r, bool& fast) {
+  const float amax = __uint_as_float(ab);
+  float sc = (scale_mode == 1) ? amax * (1.0f / 448.0f) : amax / 448.0f;
+  if (sc == 0.0f) sc = 1.0f;
+  s = sc;
+  r = 1.0f / sc;
+  fast = ab == 0 || (ab >= kFastMinAmaxBits && ab < 0x7F800000u);
+}
+
 // ---------------------------------------------------------------- wave reductions
 // DPP row rotate (within each 16-lane row).
 template <int N>

@@ -56,6 +56,9 @@ SIGNATURES = {
     "sdv_paged_attention_phases": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _P,
                                                   _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                                   _P, _SZ, _P, _P, _I32]),
+    "sdv_paged_attention_append": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _P,
+                                                  _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+                                                  _P, _SZ, _P, _P, _P, _P, _I64, _I32, _P]),
     "sdv_fp8_encode": (ctypes.c_int, [_P, _P, _I64, _P]),
     "sdv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "sdv_abi_version": (ctypes.c_int, []),

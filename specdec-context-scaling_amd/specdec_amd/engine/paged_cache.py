@@ -164,6 +164,26 @@ class PagedKVCache:
         for b in range(B):
             self.lengths[b] = starts[b] + S
 
+    def append_attend(self, layer: int, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                      starts: list[int] | None = None, *, q_token_major: bool = False,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+        """append(layer, k_new, v_new, starts) then attend(layer, q) in one call
+        (sdv_paged_attention_append): the same pages and output, one launch on the single-launch
+        path.  k_new/v_new BF16 (B, S, KV, D); q (B, H, S, D) (or (B, S, H, D))."""
+        B, S = k_new.shape[0], k_new.shape[1]
+        starts = list(self.lengths) if starts is None else list(starts)
+        for b in range(B):
+            self.reserve(b, starts[b] + S)
+        slots = self.slot_mapping(starts, S)
+        for b in range(B):
+            self.lengths[b] = starts[b] + S
+        kp, vp, vs = self.layer(layer)
+        shp = (B * S, self.kv_heads, self.head_dim)
+        return ops.paged_attention(q, kp, vp, vs, self.block_table(), self.seq_lens_tensor(), max(self.lengths),
+                                   q_token_major=q_token_major, out=out,
+                                   append=(k_new.reshape(shp), v_new.reshape(shp), slots),
+                                   scale_mode=self.scale_mode)
+
     def varlen_slots(self, lengths: list[int]) -> torch.Tensor:
         """int32 (sum(lengths),) slots of positions 0..lengths[b]-1 of each sequence in turn."""
         out = []

@@ -218,7 +218,9 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
                     block_table: torch.Tensor, seq_lens: torch.Tensor, max_seq_len: int, *,
                     q_token_major: bool = False, out: torch.Tensor | None = None,
                     workspace_tensor: torch.Tensor | None = None,
-                    phases: int = _native.PHASE_ALL) -> torch.Tensor:
+                    phases: int = _native.PHASE_ALL,
+                    append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+                    scale_mode: str = "div") -> torch.Tensor:
     """GQA attention of q over paged BF16 K / FP8 V.
 
     q: BF16 (B, H, S, D) (or (B, S, H, D) with q_token_major=True); a leading layer dimension
@@ -226,6 +228,10 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
     block_table int32 (B, max_blocks); seq_lens int32 (B,) = context length including the S
     new tokens, each <= max_seq_len.  Returns out shaped like q (BF16).
     ``phases`` (profiling) runs a subset of the three launches; see sdv_paged_attention_phases.
+    ``append`` = (k_new, v_new, slot_mapping): first write the S new tokens of every sequence
+    into the pages (as quant_append with ``scale_mode`` would; k_new/v_new BF16 (B*S, KV, D),
+    or (L, B*S, KV, D) with layers, token b*S + i at position seq_lens[b] - S + i), in the same
+    call (sdv_paged_attention_append).
     """
     lib = _native.load()
     _need(q, "q", (torch.bfloat16,), ndim=(4, 5))
@@ -271,6 +277,28 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
     args = (_p(q), _p(k_pages), _p(v_pages), _p(v_scales), nb, per(k_pages), per(v_pages), per(v_scales),
             _p(block_table), block_table.shape[1], _p(seq_lens), L, B, H, kv, S, d, max_seq_len,
             int(bool(q_token_major)), _p(workspace_tensor), workspace_tensor.numel(), _p(out), _stream(dev))
+    if append is not None:
+        if phases != _native.PHASE_ALL:
+            raise ValueError("append runs with the whole call (phases=PHASE_ALL)")
+        if scale_mode not in _SCALE_MODES:
+            raise ValueError(f"scale_mode must be one of {sorted(_SCALE_MODES)}")
+        k_new, v_new, slots = append
+        want = ((L,) if layered else ()) + (B * S, kv, d)
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            _need(t, name, (torch.bfloat16,), dev)
+            if tuple(t.shape) != want:
+                _fail(f"{name} {tuple(t.shape)} != {want}")
+        _need(slots, "slot_mapping", (torch.int32,), dev, ndim=(1,))
+        if slots.shape[0] != B * S:
+            _fail(f"slot_mapping {tuple(slots.shape)} needs {B * S} entries")
+        if k_new.data_ptr() % 16:
+            k_new = k_new.clone()
+        if v_new.data_ptr() % 16:
+            v_new = v_new.clone()
+        st = lib.sdv_paged_attention_append(*args[:-1], _p(k_new), _p(v_new), _p(slots), per(v_new),
+                                            _SCALE_MODES[scale_mode], args[-1])
+        _native.check(st, "sdv_paged_attention_append")
+        return out
     if phases == _native.PHASE_ALL:
         st = lib.sdv_paged_attention(*args)
     else:

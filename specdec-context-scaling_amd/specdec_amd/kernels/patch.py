@@ -136,7 +136,6 @@ def _fp8v_forward(self, x, cos, sin, cache=None):
         t0 = int(cache["k"].shape[2])          # logical length (a trim may have shortened it)
         for i in range(b):
             pool.set_length(i, t0)
-    pool.append(0, k.transpose(1, 2), v.transpose(1, 2), starts=[t0] * b)
     T = t0 + s
 
     # the decision is recorded as the engine would record it; both paths run on libsdv
@@ -144,7 +143,9 @@ def _fp8v_forward(self, x, cos, sin, cache=None):
     path, reason = decide(phase, s)
     record(path, phase, s, T, reason, H, KV, D)
 
-    out = pool.attend(0, q.transpose(1, 2).contiguous(), q_token_major=True)   # (b, s, H, D)
+    # append the s new tokens (quantized V, BF16 K) and attend over the context, one call
+    out = pool.append_attend(0, q.transpose(1, 2).contiguous(), k.transpose(1, 2), v.transpose(1, 2),
+                             starts=[t0] * b, q_token_major=True)   # (b, s, H, D)
     out = out.view(b, s, H * D)
     new = pages.layer_dict(T)
     if cache is None:

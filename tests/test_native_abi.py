@@ -89,6 +89,24 @@ def test_quant_host_validation(lib):
     assert _quant(lib, n=0) == _native.SDV_OK                  # nothing to do, no launch
 
 
+def test_append_attention_host_validation(lib):
+    def f(**kw):
+        a = dict(q=P, k=P, v=P, s=P, nb=8, kls=0, vls=0, sls=0, bt=P, mb=4, sl=P, L=1, B=1, H=12, KV=2, S=1,
+                 D=128, T=64, tm=0, ws=P, wsb=1 << 30, out=P, kn=P, vn=P, slots=P, nls=0, mode=0, st=N)
+        a.update(kw)
+        return lib.sdv_paged_attention_append(a["q"], a["k"], a["v"], a["s"], a["nb"], a["kls"], a["vls"], a["sls"],
+                                              a["bt"], a["mb"], a["sl"], a["L"], a["B"], a["H"], a["KV"], a["S"],
+                                              a["D"], a["T"], a["tm"], a["ws"], a["wsb"], a["out"], a["kn"], a["vn"],
+                                              a["slots"], a["nls"], a["mode"], a["st"])
+    assert f(kn=N) == _native.SDV_ERR_NULL
+    assert f(slots=N) == _native.SDV_ERR_NULL
+    assert f(q=N) == _native.SDV_ERR_NULL                         # the attention checks apply
+    assert f(mode=5) == _native.SDV_ERR_UNSUPPORTED
+    assert f(vn=ctypes.c_void_p(0x1008)) == _native.SDV_ERR_ALIGN
+    assert f(L=2, nls=8) == _native.SDV_ERR_SHAPE                   # layer stride below one layer
+    assert f(D=96) == _native.SDV_ERR_UNSUPPORTED
+
+
 def test_quant_tiles_host_validation(lib):
     def q(**kw):
         a = dict(v=P, k=N, sl=P, n=16, KV=2, D=128, gs=128, L=1, ils=0, kp=P, vp=P, vs=P, nb=8, kls=0, vls=0,

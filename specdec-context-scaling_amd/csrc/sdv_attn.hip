@@ -941,12 +941,12 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int64_t pstride = (int64_t)a.R * D;  // floats per item
   float* lparts = reinterpret_cast<float*>(smem + lay.parts);
   float2* lgs = reinterpret_cast<float2*>(smem + lay.gstats);  // per row: group (max, 1/sum)
-  // the group's statistics: wavefront 0 waits until all nvq items have published, merges them
+  // the group's statistics: wavefront nt waits until all nvq items have published row tile nt, merges them
   // in a fixed order -- item slice j takes items j, j+nsl, ..., then a fixed tree -- and shares
   // (max, 1/sum) of each row through LDS, so every wavefront and workgroup of the group gets
   // identical values.  The other wavefronts' V loads stay in flight across the barrier.
   auto group_stats = [&](float (&gm)[NT], float (&ginv)[NT]) {
-    if (wave == 0) {
+    if (wave < NT) {  // wavefront nt polls and merges row tile nt (all tiles at once)
       constexpr int PB = D == 128 ? 16 : 8;  // entries in flight per lane (registers allow)
       // lane = (item slice, row): 16 rows x 4 slices, or 8 x 8 when the rows fit in 8 and the
       // group has more than 8 items, so that more lanes share the merges (one layer at 8K, 64
@@ -956,8 +956,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       const int rl = narrow ? (lane & 7) : n, sl = narrow ? (lane >> 3) : g;
       const int ne = (nvq - sl + nsl - 1) / nsl;           // items of this slice (<= PB)
       const int ne_max = (nvq + nsl - 1) / nsl;            // wave-uniform loop bound
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
+      {
+        const int nt = wave;
         const int rr = nt * 16 + rl;
         const float2* fp = fs + (int64_t)item0 * 64 + (rr < a.R ? rr : 0);
         float m = -INFINITY, l = 0.0f;
@@ -1297,8 +1297,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int nld = w * nvq;                 // chunks this workgroup reads
   float4* red = reinterpret_cast<float4*>(smem + lay.red);
   __syncthreads();  // LDS is reused below
-  for (int e0 = 0; e0 < nld; e0 += NTHR) {  // workgroup-uniform
-    const int e = e0 + tid;
+  auto poll_chunks_one = [&]() {  // at most one chunk per thread
+    const int e = tid;
     const bool act = e < nld;
     const int cc = act ? e / w : 0, o = act ? e - cc * w : 0;
     const int off = (int)(((int64_t)(item0 + cc) * pstride + 4 * (lo + o)) * 4);
@@ -1316,7 +1316,51 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       if (!ready) v = __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 16);
     }
     if (act) red[e] = part_dec(v);
-  }
+  };
+  // Every chunk an owner reads is loaded before any is polled: with at most one chunk per
+  // thread (decode) one load each; otherwise (verify: 960 chunks per owner) up to kOutLoads
+  // per thread, so the rounds do not wait for each other.
+  constexpr int kOutLoads = 4;
+  auto poll_chunks_many = [&]() {  // several chunks per thread, all in flight before polling
+    for (int e0 = 0; e0 < nld; e0 += NTHR * kOutLoads) {  // workgroup-uniform
+      u32x4_t v[kOutLoads];
+      int off[kOutLoads];
+#pragma unroll
+      for (int r = 0; r < kOutLoads; ++r) {
+        const int e = e0 + r * NTHR + tid;
+        const bool act = e < nld;
+        const int cc = act ? e / w : 0, o = act ? e - cc * w : 0;
+        off[r] = (int)(((int64_t)(item0 + cc) * pstride + 4 * (lo + o)) * 4);
+        v[r] = (u32x4_t){1u, 1u, 1u, 1u};
+        if (act) v[r] = __builtin_amdgcn_raw_buffer_load_b128(prs, off[r], 0, 16);
+      }
+      unsigned spins = 0;
+      for (;;) {
+        bool ready = true;
+#pragma unroll
+        for (int r = 0; r < kOutLoads; ++r) ready = ready && v[r][0] != 0u && v[r][1] != 0u && v[r][2] != 0u && v[r][3] != 0u;
+        if (__ballot(!ready) == 0) break;
+        if (++spins > (1u << 20)) {
+          if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int r = 0; r < kOutLoads; ++r)
+          if (!(v[r][0] != 0u && v[r][1] != 0u && v[r][2] != 0u && v[r][3] != 0u))
+            v[r] = __builtin_amdgcn_raw_buffer_load_b128(prs, off[r], 0, 16);
+      }
+#pragma unroll
+      for (int r = 0; r < kOutLoads; ++r) {
+        const int e = e0 + r * NTHR + tid;
+        if (e < nld) red[e] = part_dec(v[r]);
+      }
+    }
+  };
+  if (nld <= NTHR)  // workgroup-uniform
+    poll_chunks_one();
+  else
+    poll_chunks_many();
   __syncthreads();
   // Sum over the items in a fixed order.  For 16 items or more and enough threads, in two
   // levels: thread (sg, o) adds the items of segment sg (about sqrt(nvq) of them) in order,

@@ -82,7 +82,8 @@ __device__ __forceinline__ int seq_len_of(const AttnArgs& a, int b) {
 // exp(x) as 2^(x * log2 e) on v_exp_f32.  The rounding of x * log2 e costs at most
 // |x| * 2^-24 relative, far below one BF16 step of the probabilities it feeds (and below
 // the fp32 summation noise of L); exp(-inf) = 0.
-__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
 __device__ __forceinline__ void merge_fast(float& m, float& l, float m2, float l2) {
   const float mn = fmaxf(m, m2);
@@ -687,11 +688,25 @@ __device__ __forceinline__ float4 part_dec(u32x4_t w) {
 // 8K: 23.7 us vs 25.5 us).
 template <int D, int NT>
 constexpr int fused_waves() { return NT == 1 ? (D == 128 ? 8 : 16) : NT == 2 ? 8 : 4; }
-constexpr int kVStages = 6;  // p.V stages in flight per wavefront
+#ifndef SDV_TUNE_WIDE_MIN
+#define SDV_TUNE_WIDE_MIN 64
+#endif
+constexpr int kVStages = 6;  // p.V stages in flight per wavefront (one 16-dimension tile each)
 // dimension-tile groups of the static p.V split (several row tiles): wavefront w takes the
-// 16-dimension tiles of group w % ntg for block part w / ntg (measured on 28-layer verify at
-// 8K: 2 or 4 groups of wider tiles, with 3 to 6 stages, no faster than one tile per wavefront)
+// 16-dimension tiles of group w % ntg for block part w / ntg
 __host__ __device__ constexpr int fused_ntg(int D, int W) { return D / 16 < W ? D / 16 : W; }
+// Two row tiles with items of at least kWideMinBlocks blocks: two groups of wider tiles
+// (D/32 dimensions per wavefront over a quarter of the blocks).  The conversion of the codes,
+// the scale broadcasts, the address arithmetic and the probability reads are then shared by
+// four tiles instead of one; the verify p.V is bound by that VALU work (per-wavefront end
+// times on 28 layers at 8K: the second wavefront of every SIMD ends 2.4 us after the first).
+// Small items keep one tile per wavefront: with a few blocks per part the parts' sum costs
+// more than it saves (28 layers, S=5: 8K 49.6-51.9 -> 48.4-48.9 us; 2K and 4K equal within
+// noise; one layer 1.1 us slower at 8K with 16 blocks per item).
+constexpr int kWideMinBlocks = SDV_TUNE_WIDE_MIN;
+__host__ __device__ constexpr int fused_ntg_wide(int D, int W, int NT) {
+  return NT == 2 && fused_ntg(D, W) > 2 ? 2 : fused_ntg(D, W);
+}
 
 // dynamic LDS of a fused workgroup with items of up to `maxblk` blocks (byte offsets).  With
 // one row tile the p.V work is claimed in units and each unit's result gets an LDS slot
@@ -699,8 +714,8 @@ __host__ __device__ constexpr int fused_ntg(int D, int W) { return D / 16 < W ? 
 struct FusedLds {
   int scores, bstats, pages, gstats, parts, red, total;
 };
-__host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool claim_pv) {
-  const int ntg = fused_ntg(D, W), tp = W / ntg;
+__host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool claim_pv, int ntg) {
+  const int tp = W / ntg;
   FusedLds l;
   l.scores = 0;                                                            // [R][16*maxblk + 8] bf16
   l.bstats = (l.scores + R * (maxblk * kBlock + 8) * 2 + 15) & ~15;        // [maxblk][R] float2
@@ -724,11 +739,11 @@ __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, i
   return l;
 }
 
-template <int D, int NT, int W>
+template <int D, int NT, int W, int NTG>
 __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   constexpr int NTHR = 64 * W;
   constexpr int KK = D / 32, DT = D / 16;
-  constexpr int NTG = fused_ntg(D, W);  // dimension-tile groups in p.V
+  // NTG: dimension-tile groups in p.V (static split)
   constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
   constexpr int TP = W / NTG;            // block parts in p.V
 #ifndef SDV_TUNE_QK_CLAIM
@@ -774,7 +789,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int nvq = min(n_g, (int)(((int64_t)nblk_seq * n_g + a.f_gb - 1) / a.f_gb));
 
   constexpr bool kClaimPV = NT == 1;  // one row tile: p.V units claimed like q.k^T blocks
-  const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kClaimPV);
+  const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kClaimPV, NTG);
   char* smem = reinterpret_cast<char*>(smem_u4);
   uint16_t* lsc = reinterpret_cast<uint16_t*>(smem + lay.scores);  // row r: scores of query row r
   const int lrow = a.f_maxblk * kBlock + 8;
@@ -1017,10 +1032,13 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       const uint4 w4 = *pp;
       const uint32_t sw[4] = {w4.x, w4.y, w4.z, w4.w};
       float pr[8];
+      // exp(s - M) as 2^(s log2 e - M log2 e), one FMA per score (28 layers at 8K, S=5: about
+      // 0.5 us less VALU time than a subtract and a multiply)
+      const float nml = -st.x * kLog2e;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float sc = (i & 1) ? bf16_hi(sw[i >> 1]) : bf16_lo(sw[i >> 1]);
-        pr[i] = fast_exp(sc - st.x) * st.y;
+        pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc, kLog2e, nml)) * st.y;  // -inf score -> 0
       }
       *pp = make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]), pack_bf16x2(pr[4], pr[5]),
                        pack_bf16x2(pr[6], pr[7]));
@@ -1165,15 +1183,26 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       for (int dtw = 0; dtw < DTW; ++dtw) s.code[dtw] = load_stream16(vp + dtw * 16 * kBlock);
       s.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
     };
-    // kVStages stages of V in flight per wavefront: a stage is only 1 KiB of codes per 16-dim
-    // tile, so a deep ring keeps enough bytes moving; loads past the end read block 0 (the
+    // kVStages stages of V in flight per wavefront (3 with wider tiles): a stage is only 1 KiB
+    // of codes per 16-dim tile, so a deep ring keeps enough bytes moving; loads past the end read block 0 (the
     // wait counters stay exact) and are never computed
-    constexpr int SD = kVStages;
+    constexpr int SD = DTW >= 2 ? 3 : kVStages;
     Stage ring[SD];
+    // With the wide split (large items) the polling wavefronts load their ring only after
+    // the group statistics: a poll load queued behind the ring returns once the ring has
+    // (first poll check 3.2 us after the publish against 1.6 us for decode; 28 layers at 8K:
+    // 48.8-49.5 -> 47.7-47.8 us).  Small items lose by it (one layer: +0.9 us): their wait
+    // is short and their ring is most of their p.V.
+    constexpr bool kPollFirst = NTG < fused_ntg(D, W);
+    if (!kPollFirst || wave >= NT) {  // wave-uniform
   #pragma unroll
-    for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
-
+      for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
+    }
     group_stats(gm, ginv);
+    if (kPollFirst && wave < NT) {
+  #pragma unroll
+      for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
+    }
     prob_pass();
     __syncthreads();
     f32x4 acc[DTW][NT];
@@ -1500,7 +1529,7 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
 // Resident workgroup capacity of fused_kernel<D, NT> with `lds` bytes of dynamic LDS on the
 // current device (cached per device and 4 KiB LDS bucket); 0 when the device cannot run it.
 // Above 64 KiB of dynamic LDS the kernel's limit is raised first (once per device and size).
-template <int D, int NT, int W>
+template <int D, int NT, int W, int NTG>
 static int fused_capacity(size_t lds) {
   constexpr int kBuckets = 41;  // 0 .. 160 KiB
   static std::atomic<int> cache[64][kBuckets];
@@ -1511,13 +1540,13 @@ static int fused_capacity(size_t lds) {
   int cap = cache[dev][bucket].load(std::memory_order_relaxed);
   if (cap > 0) return cap;
   if ((size_t)bucket * 4096 > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(fused_kernel<D, NT, W>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fused_kernel<D, NT, W, NTG>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, bucket * 4096) != hipSuccess) {
     (void)hipGetLastError();  // leave no error behind for the launch status check
     return 0;
   }
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, NT, W>, 64 * W,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel<D, NT, W, NTG>, 64 * W,
                                                    (size_t)bucket * 4096) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
     (void)hipGetLastError();
@@ -1533,7 +1562,7 @@ static int fused_capacity(size_t lds) {
 }
 
 struct FusedShape {
-  int gb, base, extra, maxblk, grid;
+  int gb, base, extra, maxblk, grid, ntg;
   size_t lds;
 };
 
@@ -1553,14 +1582,17 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
   const int max_items = min(min(kFusedGroupItems, gb), max(1, gb / kFusedMinBlocks));
   // items whose fp32 partials fit the sync area
   const int part_cap = (int)(kSyncPartBytes / ((size_t)R * D * 4));
-  int cap = min(part_cap, fused_capacity<D, NT, W>((size_t)fused_lds_layout(R, D, 1, W, NT == 1).total));
+  constexpr int NTGN = fused_ntg(D, W), NTGW = fused_ntg_wide(D, W, NT);
+  int cap = min(part_cap, fused_capacity<D, NT, W, NTGN>((size_t)fused_lds_layout(R, D, 1, W, NT == 1, NTGN).total));
   for (int iter = 0; iter < 4; ++iter) {
     if (cap < G) return false;
     const int base = min(max_items, cap / G);
     const int maxblk = (gb + base - 1) / base;
-    const size_t lds = (size_t)fused_lds_layout(R, D, maxblk, W, NT == 1).total;
+    const int ntg = maxblk >= kWideMinBlocks ? NTGW : NTGN;
+    const size_t lds = (size_t)fused_lds_layout(R, D, maxblk, W, NT == 1, ntg).total;
     if (lds > 160 * 1024) return false;
-    const int cap2 = min(part_cap, fused_capacity<D, NT, W>(lds));
+    const int cap2 =
+        min(part_cap, ntg == NTGN ? fused_capacity<D, NT, W, NTGN>(lds) : fused_capacity<D, NT, W, NTGW>(lds));
     if (cap2 < cap) {  // a wider item needs more LDS: the device holds fewer of them
       cap = cap2;
       continue;
@@ -1577,6 +1609,7 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
     f->extra = extra;
     f->maxblk = maxblk;  // groups with base+1 items have smaller items
     f->grid = grid;
+    f->ntg = ntg;
     f->lds = lds;
     return true;
   }
@@ -1592,7 +1625,11 @@ static bool try_fused(AttnArgs a, const Plan& p, hipStream_t st) {
   a.f_base = f.base;
   a.f_extra = f.extra;
   a.f_maxblk = f.maxblk;
-  hipLaunchKernelGGL((fused_kernel<D, NT, W>), dim3((unsigned)f.grid), dim3(64 * W), f.lds, st, a);
+  constexpr int NTGN = fused_ntg(D, W), NTGW = fused_ntg_wide(D, W, NT);
+  if (f.ntg == NTGN)
+    hipLaunchKernelGGL((fused_kernel<D, NT, W, NTGN>), dim3((unsigned)f.grid), dim3(64 * W), f.lds, st, a);
+  else
+    hipLaunchKernelGGL((fused_kernel<D, NT, W, NTGW>), dim3((unsigned)f.grid), dim3(64 * W), f.lds, st, a);
   return true;
 }
 

@@ -315,6 +315,21 @@ def test_multi_layer_verify_s5(cuda_device, t):
     _check_multi_layer(cuda_device, cache, 12, 5, (0, 27), (0,), f"verify T={t}", seed=511)
 
 
+@pytest.mark.parametrize("layers,h,d,lens", [(1, 12, 128, [32768, 9000]), (1, 12, 64, [32768]), (16, 12, 128, [8192])])
+def test_verify_wide_split(cuda_device, layers, h, d, lens):
+    """Verify (S=5, two row tiles) on items of 64 blocks or more, where p.V splits wider
+    dimension tiles over block parts and the polling wavefronts load V after the group wait:
+    a ragged pair (items past the short sequence's end own nothing), D=64, and 16 layers."""
+    announce(f"attn verify wide split L={layers} {h}/2/{d} lens={lens}")
+    grid = ops.single_launch_workgroups(layers, len(lens), h, 2, 5, d, max(lens))
+    groups = layers * len(lens) * 2
+    assert grid > 0 and grid % groups == 0
+    assert -(-max(lens) // 16) // (grid // groups) >= 64  # blocks per item
+    cache = _filled_cache(cuda_device, layers, 2, d, lens, seed=560 + layers + d)
+    _check_multi_layer(cuda_device, cache, h, 5, tuple(sorted({0, layers - 1})), tuple(range(len(lens))),
+                       f"wide L={layers} d={d}", seed=561)
+
+
 def test_multi_layer_batch32_ragged(cuda_device):
     """Config 4: B=32 contexts U{2048..32768}, fragmented pool, 1% outlier V channels x20,
     28 layers in one launch; the shortest, the longest and the first sequence are checked."""

@@ -867,16 +867,23 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
           if (row < a.R)
             *reinterpret_cast<uint2*>(lsc + row * lrow + jb * kBlock + 4 * g) =
                 make_uint2(pack_bf16x2(s4[0], s4[1]), pack_bf16x2(s4[2], s4[3]));
-          // this block's (max, sum) of the row: the four lane groups combine in a fixed tree
+          // this block's (max, sum) of the row: the block max over the four lane groups first,
+          // then every exp against it and a fixed sum tree (lower lane first, so the lanes of
+          // a pair hold identical bits).  Against a (max, sum) merge per lane-group pair this
+          // spends no rescaling exps: the q.k^T phase of verify is partly VALU-bound.
+          float2 pm = lane_pair<16>(mt);
+          float M = fmaxf(pm.x, pm.y);
+          pm = lane_pair<32>(M);
+          M = fmaxf(pm.x, pm.y);
+          const float nml = M == -INFINITY ? 0.0f : -M * kLog2e;  // empty row: every exp is 0
           float l = 0.0f;
-          if (mt != -INFINITY) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) l += fast_exp(s4[i] - mt);
-          }
-          float m = mt;
-          merge_lanes<16>(m, l);
-          merge_lanes<32>(m, l);
-          if (g == 0 && row < a.R) bst[jb * a.R + row] = make_float2(m, l);
+          for (int i = 0; i < 4; ++i) l += __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml));
+          float2 pl = lane_pair<16>(l);
+          l = pl.x + pl.y;
+          pl = lane_pair<32>(l);
+          l = pl.x + pl.y;
+          if (g == 0 && row < a.R) bst[jb * a.R + row] = make_float2(M, l);
         }
       }
     };

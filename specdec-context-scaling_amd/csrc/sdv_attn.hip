@@ -200,10 +200,13 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
         lsc[wave][nt * 16 + n][(j0 + u) * 4 + g] =
             make_uint2(pack_bf16x2(s4[0], s4[1]), pack_bf16x2(s4[2], s4[3]));
         if (mt != -INFINITY) {
-          const float mn = fmaxf(m_run[nt], mt);
-          float l = (m_run[nt] == -INFINITY) ? 0.0f : l_run[nt] * fast_exp(m_run[nt] - mn);
+          // exp(x - mn) as 2^(x log2 e - mn log2 e): one FMA per exp
+          const float mn = fmaxf(m_run[nt], mt), nml = -mn * kLog2e;
+          float l = (m_run[nt] == -INFINITY)
+                        ? 0.0f
+                        : l_run[nt] * __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[nt], kLog2e, nml));
 #pragma unroll
-          for (int i = 0; i < 4; ++i) l += fast_exp(s4[i] - mn);
+          for (int i = 0; i < 4; ++i) l += __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml));
           m_run[nt] = mn;
           l_run[nt] = l;
         }

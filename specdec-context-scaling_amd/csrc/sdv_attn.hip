@@ -1198,18 +1198,22 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     // wait counters stay exact) and are never computed
     constexpr int SD = DTW >= 2 ? 3 : kVStages;
     Stage ring[SD];
-    // With the wide split (large items) the polling wavefronts load their ring only after
-    // the group statistics: a poll load queued behind the ring returns once the ring has
-    // (first poll check 3.2 us after the publish against 1.6 us for decode; 28 layers at 8K:
-    // 48.8-49.5 -> 47.7-47.8 us).  Small items lose by it (one layer: +0.9 us): their wait
-    // is short and their ring is most of their p.V.
-    constexpr bool kPollFirst = NTG < fused_ntg(D, W);
-    if (!kPollFirst || wave >= NT) {  // wave-uniform
+    // With items of kPollFirstMinBlocks blocks or more the polling wavefronts load their
+    // ring only after the group statistics: a poll load queued behind the ring returns once
+    // the ring has (first poll check 3.2 us after the publish against 1.6 us for decode; 28
+    // layers at 8K: 48.8-49.5 -> 47.7-47.8 us).  Small items lose by it (one layer: +0.9
+    // us): their wait is short and their ring is most of their p.V.
+#ifndef SDV_TUNE_PF_MIN
+#define SDV_TUNE_PF_MIN 32
+#endif
+    constexpr int kPollFirstMinBlocks = SDV_TUNE_PF_MIN;
+    const bool poll_first = a.f_maxblk >= kPollFirstMinBlocks;  // workgroup-uniform
+    if (!poll_first || wave >= NT) {  // wave-uniform
   #pragma unroll
       for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
     }
     group_stats(gm, ginv);
-    if (kPollFirst && wave < NT) {
+    if (poll_first && wave < NT) {
   #pragma unroll
       for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
     }

@@ -5,8 +5,10 @@
  * All tensor arguments are DEVICE pointers owned by the caller; the library allocates
  * nothing per call.  Every entry point validates its arguments on the host, returns
  * SDV_OK (0) or a negative status, launches asynchronously on `stream` (a hipStream_t,
- * NULL = the legacy default stream) and is re-entrant (no mutable global state; calls
- * that share a workspace buffer must be ordered on one stream).
+ * NULL = the legacy default stream) and is re-entrant (the only process-wide state is an
+ * atomic call counter that tags single-launch calls and the wait bound set by
+ * sdv_attention_set_wait_limit; calls that share a workspace buffer must be ordered on one
+ * stream).
  *
  * Paged cache layout (one layer; layers sit `*_layer_stride` elements apart):
  *   k_pages  [num_blocks][kv_heads][head_dim/8][16][8]  bf16: token t, dim d of a page sits at
@@ -111,12 +113,42 @@ size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q
 /*
  * Zero the workspace's synchronisation area (its first SDV_SYNC_BYTES bytes) on `stream`.
  * Call it once after allocating a workspace and before its first sdv_paged_attention; every
- * call leaves the area zero again.  The area's first 32-bit word counts waits of the
- * single-launch path that expired (0 unless its workgroups could not all be resident).
- * No counterpart in the reference (it has no workspace).
+ * call that completes normally leaves the area zero again.  No counterpart in the reference
+ * (it has no workspace).
+ *
+ * The single-launch path exchanges (max, sum) statistics and fp32 partials between
+ * workgroups through this area as 64-bit (value, call tag) words; a reader takes a word only
+ * when it carries its own call's tag, so a word an earlier call left behind is never read
+ * as current.  Its waits are bounded (they only expire when the grid's workgroups cannot all
+ * be resident at once: another process holding CUs, a CU mask): an expired wait makes the
+ * outputs it could not complete NaN and counts in word 0 of the area.  A call recorded into
+ * a HIP graph (its replays reuse one tag) that expires also sets word 1; while it is set,
+ * every graph-recorded call writes NaN to all of its outputs and counts itself instead of
+ * running, until sdv_attention_workspace_init clears the area.  Eager calls take a fresh tag
+ * each and are unaffected.
  */
-#define SDV_SYNC_BYTES 10486016
+#define SDV_SYNC_BYTES 12583168
 int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Read words 0 and 1 of a workspace's synchronisation area: `failures` = expired waits and
+ * refused calls of the single-launch path since the last sdv_attention_workspace_init, and
+ * `poisoned` != 0 when graph-recorded calls are refused (see above).  Synchronises `stream`
+ * (a device-to-host copy); not for use while a graph is being recorded.  No counterpart in
+ * the reference.
+ */
+int sdv_attention_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* failures,
+                                   uint32_t* poisoned, void* stream);
+
+/*
+ * Bound of every cross-workgroup wait of the single-launch path, in polls, for calls issued
+ * after this one; 0 restores the default (2^20 polls; a poll waits for a device-scope load,
+ * about a microsecond, so the default gives up after about a second).  A wait expires at its
+ * `polls`-th unsuccessful poll: 1 gives up at the first entry not yet published.  For tests
+ * of the failure path: a tiny bound makes waits expire while every workgroup still runs to
+ * its end.  No counterpart in the reference.
+ */
+int sdv_attention_set_wait_limit(uint32_t polls);
 
 /*
  * Which path sdv_paged_attention takes for these sizes on the current device: the number of

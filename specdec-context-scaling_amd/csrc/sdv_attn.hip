@@ -67,6 +67,10 @@ struct AttnArgs {
   const int32_t* app_slots;
   int64_t app_ls;
   int app_scale_mode;
+  // single launch: the call's tag (never 0; bit 31 set for a call recorded into a graph, whose
+  // replays reuse it) and the bound of every cross-workgroup wait, in polls
+  uint32_t tag;
+  uint32_t spin_limit;
 };
 
 __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
@@ -392,11 +396,8 @@ __device__ __forceinline__ void pv_compute(PvStage<D, NT>& st, f32x4 (&acc)[D / 
   pv_half<D, NT, 1>(st, acc, gm, ginv);
 }
 
-#ifndef SDV_PV_WAVES_PER_EU  // tuning builds: occupancy floor the compiler must fit pv_kernel into
-#define SDV_PV_WAVES_PER_EU 1
-#endif
 template <int D, int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SDV_PV_WAVES_PER_EU))) void pv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
   constexpr int DT = D / 16;  // 16-dimension MFMA tiles
   constexpr int RT = NT * 16;
   __shared__ float lacc[kWaves][16][D + 4];  // +4: spread the lane groups over LDS banks
@@ -619,56 +620,74 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
 //      per (row, token); the wavefronts run p.V over the item's blocks; per-unit results
 //      are summed in LDS in order and the fp32 partial is published.
 //   3. Workgroup c of the group owns a slice of the outputs: it polls the slice of every
-//      item's partial (a published partial word is its bits + 1, so zero means "not yet"),
-//      sums it over the items in order (the result does not depend on the order workgroups
-//      finish) into the BF16 output, and clears what it read plus a share of the
-//      statistics for the next call.
+//      item's partial, sums it over the items in order (the result does not depend on the
+//      order workgroups finish) into the BF16 output, and clears what it read plus a share of
+//      the statistics for the next call.
 // Cross-workgroup data moves through device-scope (sc1) stores and loads, which bypass the
-// per-XCD L2 caches; every published word carries its own "written" mark, so no counter,
-// ticket or cache-writeback fence is needed (on gfx950 each agent-scope release costs
-// ~40 ns and serialises chip-wide; a counter round trip costs ~1.3 us across XCDs).
+// per-XCD L2 caches; no counter, ticket or cache-writeback fence is needed (on gfx950 each
+// agent-scope release costs ~40 ns and serialises chip-wide; a counter round trip costs ~1.3 us
+// across XCDs).  A word left over from an earlier call never passes for a current one:
+//   * statistics travel as 64-bit (value, call tag) words written and read with
+//     single-copy-atomic 64-bit accesses; a reader takes a word only when it carries its own
+//     call's tag.  Eager calls get a fresh tag each; the replays of a graph reuse their recorded
+//     tag, so the owners clear the statistics they consumed and every replay starts clean.
+//   * a partial word holds the float's bits + 1 (0 means "not yet written").  An item zeroes
+//     its own partial slot at the start of the call and waits for those stores to complete
+//     before it publishes its statistics; an owner reads partials only after it has taken every
+//     item's statistics of this call, so whatever it reads in a slot was written by that item in
+//     this call.
 // Deadlock freedom: a workgroup publishes before it waits and the grid never exceeds the
 // device's resident capacity (occupancy query), so every entry a wait needs comes from a
-// running workgroup.  Waits are bounded; on expiry they count an error in word 0 of the
-// synchronisation area and continue.
+// running workgroup.  If that assumption fails (another process holds CUs, a CU mask), waits
+// are bounded (a.spin_limit polls): an expired wait counts in word 0 of the synchronisation
+// area, turns the affected outputs into NaN (its group's statistics, or the owner's output
+// slice) and skips the clears.  A graph-recorded call that expires also sets word 1: from
+// then on every graph-recorded call writes NaN to all of its outputs and counts itself
+// instead of running (its replays would reuse the tag of the words that may be left over)
+// until sdv_attention_workspace_init clears the area; eager calls are unaffected.
 constexpr int kFusedMaxItems = 4096;    // published (max, sum) rows: 64 per item
 constexpr int kFusedMaxChunks = 64;     // items per group
-#ifndef SDV_FUSED_MIN_BLOCKS  // tuning builds: smallest item the planner aims for
-#define SDV_FUSED_MIN_BLOCKS 1
-#endif
-constexpr int kFusedMinBlocks = SDV_FUSED_MIN_BLOCKS;
 // Most items per group.  A one-layer call is split as finely as this allows; 32 items (4
 // blocks each at T=2048, 16 at 8K) beat 64 (10.2-10.5 vs 10.9 us at 2K; 28 per-layer calls in
 // a graph 13.0 vs 13.4 us per layer at 8K): fewer entries to merge and sum per group.
-#ifndef SDV_FUSED_GROUP_ITEMS  // tuning builds: other caps
-#define SDV_FUSED_GROUP_ITEMS 32
-#endif
-constexpr int kFusedGroupItems = SDV_FUSED_GROUP_ITEMS;
+constexpr int kFusedGroupItems = 32;
 static_assert(kFusedGroupItems <= kFusedMaxChunks, "the output stage holds kFusedMaxChunks items");
-#ifndef SDV_FUSED_MAX_PER_CU  // tuning builds: resident decode workgroups per CU
-#define SDV_FUSED_MAX_PER_CU 1
-#endif
-constexpr int kFusedMaxPerCU = SDV_FUSED_MAX_PER_CU;
-constexpr size_t kSyncHeadBytes = 256;  // word 0: expired waits
-constexpr size_t kSyncStatsBytes = (size_t)kFusedMaxItems * 64 * 8;
-constexpr size_t kSyncPartBytes = (size_t)8 << 20;  // fp32 partials of one call's items
+// Resident workgroups per CU the planner allows (the occupancy query may allow more).  Decode
+// (one row tile) keeps one workgroup per CU: a second resident workgroup only splits the CU's
+// bandwidth between two items of the same size (28 layers at 8K: 504 workgroups 42.7-43.1 us
+// against 224 at 39.4 us).  The D=128 verify shapes keep the counts they were tuned at (one for
+// two row tiles, two for three or four).
+template <int D, int NT>
+constexpr int fused_max_per_cu() { return NT == 1 ? 1 : D == 128 ? (NT == 2 ? 1 : 2) : 64; }
+constexpr size_t kSyncHeadBytes = 256;  // word 0: expired waits and refused calls; word 1: graph poison
+constexpr size_t kSyncStatsBytes = (size_t)kFusedMaxItems * 64 * 16;  // (max, tag), (sum, tag) per row
+constexpr size_t kSyncPartBytes = (size_t)8 << 20;  // fp32 partials (bits + 1) of one call's items
 constexpr size_t kSyncBytes = kSyncHeadBytes + kSyncStatsBytes + kSyncPartBytes;
 static_assert(kSyncBytes == SDV_SYNC_BYTES, "sdv.h states the synchronisation prefix size");
+constexpr uint32_t kTagGraph = 0x80000000u;  // tag bit of a graph-recorded call
+constexpr uint32_t kDefaultSpinLimit = 1u << 20;
 
-#define SDV_VMCNT0() __builtin_amdgcn_s_waitcnt(0x0F70)  // vmcnt(0); exp/lgkm counters untouched
-
-__device__ __forceinline__ void store_dev_f2(float2* p, float2 v) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
+  return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)tag << 32);
 }
-__device__ __forceinline__ uint64_t load_dev_u64(const float2* p) {
-  return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void store_dev_u64(uint64_t* p, uint64_t w) {
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float2* sync_stats(const AttnArgs& a) {
-  return reinterpret_cast<float2*>(reinterpret_cast<char*>(a.sync) + kSyncHeadBytes);
+__device__ __forceinline__ uint64_t load_dev_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ bool has_tag(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ float word_value(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)w); }
+// statistics of (item, row): words 2*(item*64 + row) (max) and +1 (sum)
+__device__ __forceinline__ uint64_t* sync_stats(const AttnArgs& a) {
+  return reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(a.sync) + kSyncHeadBytes);
+}
+// partial of (item, output element o): float item * R * D + o
 __device__ __forceinline__ float* sync_parts(const AttnArgs& a) {
   return reinterpret_cast<float*>(reinterpret_cast<char*>(a.sync) + kSyncHeadBytes + kSyncStatsBytes);
+}
+__device__ __forceinline__ void count_sync_error(const AttnArgs& a) {
+  __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // A published partial word holds the float's bits + 1, so 0 always means "not yet written"
 // (the one pattern that would wrap, NaN 0xFFFFFFFF, is stored as a quiet NaN).
@@ -683,6 +702,7 @@ __device__ __forceinline__ float4 part_dec(u32x4_t w) {
   return make_float4(__builtin_bit_cast(float, w[0] - 1u), __builtin_bit_cast(float, w[1] - 1u),
                      __builtin_bit_cast(float, w[2] - 1u), __builtin_bit_cast(float, w[3] - 1u));
 }
+#define SDV_VMCNT0() __builtin_amdgcn_s_waitcnt(0x0F70)  // vmcnt(0); exp/lgkm counters untouched
 
 // wavefronts of the fused workgroup for NT row tiles.  With one row tile the workgroup is
 // alone on its CU; measured on gfx950, 8 wavefronts finish a D=128 call sooner than 16 (one
@@ -691,9 +711,6 @@ __device__ __forceinline__ float4 part_dec(u32x4_t w) {
 // 8K: 23.7 us vs 25.5 us).
 template <int D, int NT>
 constexpr int fused_waves() { return NT == 1 ? (D == 128 ? 8 : 16) : NT == 2 ? 8 : 4; }
-#ifndef SDV_TUNE_WIDE_MIN
-#define SDV_TUNE_WIDE_MIN 64
-#endif
 constexpr int kVStages = 6;  // p.V stages in flight per wavefront (one 16-dimension tile each)
 // dimension-tile groups of the static p.V split (several row tiles): wavefront w takes the
 // 16-dimension tiles of group w % ntg for block part w / ntg
@@ -706,7 +723,7 @@ __host__ __device__ constexpr int fused_ntg(int D, int W) { return D / 16 < W ? 
 // Small items keep one tile per wavefront: with a few blocks per part the parts' sum costs
 // more than it saves (28 layers, S=5: 8K 49.6-51.9 -> 48.4-48.9 us; 2K and 4K equal within
 // noise; one layer 1.1 us slower at 8K with 16 blocks per item).
-constexpr int kWideMinBlocks = SDV_TUNE_WIDE_MIN;
+constexpr int kWideMinBlocks = 64;
 __host__ __device__ constexpr int fused_ntg_wide(int D, int W, int NT) {
   return NT == 2 && fused_ntg(D, W) > 2 ? 2 : fused_ntg(D, W);
 }
@@ -749,10 +766,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   // NTG: dimension-tile groups in p.V (static split)
   constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
   constexpr int TP = W / NTG;            // block parts in p.V
-#ifndef SDV_TUNE_QK_CLAIM
-#define SDV_TUNE_QK_CLAIM 1
-#endif
-  constexpr int P = SDV_TUNE_QK_CLAIM;   // page blocks per q.k^T claim
+  constexpr int P = 1;                   // page blocks per q.k^T claim
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   extern __shared__ uint4 smem_u4[];
   __shared__ int s_next, s_next2;
@@ -790,6 +804,29 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int nbv = min(nbk, nblk_seq - blk_lo);  // item blocks inside the sequence (>= 1)
   // non-empty items of the group: item i starts at block floor(i * gb / n_g)
   const int nvq = min(n_g, (int)(((int64_t)nblk_seq * n_g + a.f_gb - 1) / a.f_gb));
+  // Output slice of this workgroup: workgroup c < nvq of the group owns 16-byte output chunks
+  // [lo, lo + w) (four outputs each); nown workgroups have a non-empty slice.
+  const int n4 = a.R * D / 4;
+  const int per = (n4 + nvq - 1) / nvq;
+  const int lo = c * per, w = max(min(n4, lo + per) - lo, 0);
+  const int nown = (n4 + per - 1) / per;
+  // NaN into this workgroup's output slice (a failed or refused call)
+  auto nan_slice = [&]() {
+    for (int o = tid; o < w; o += NTHR) {
+      const int o4 = lo + o;
+      const int row = (4 * o4) / D, d = 4 * o4 - row * D, hl = row / a.S, si = row % a.S;
+      uint16_t* dst = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(0x7FC07FC0u, 0x7FC07FC0u);
+    }
+  };
+  const bool graph_call = (a.tag & kTagGraph) != 0;
+  __shared__ int s_fail;  // a wait of this workgroup expired (or a graph-recorded call was refused)
+  // this item's partial slot starts the call zeroed: the stores are issued first and have
+  // completed (vmcnt(0) after q.k^T) before the item publishes its statistics
+  const int64_t pstride = (int64_t)a.R * D;  // floats per item
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(sync_parts(a), (short)0, (int)kSyncPartBytes, 0x00020000);
+  for (int o4 = tid; o4 < n4; o4 += NTHR)
+    __builtin_amdgcn_raw_buffer_store_b128((u32x4_t){0u, 0u, 0u, 0u}, prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
 
   constexpr bool kClaimPV = NT == 1;  // one row tile: p.V units claimed like q.k^T blocks
   const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kClaimPV, NTG);
@@ -803,7 +840,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     const int pb = btrow[blk_lo + j];
     lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
   }
-  if (tid == 0) s_next = s_next2 = 0;
+  if (tid == 0) s_next = s_next2 = s_fail = 0;
   // the group's new tokens inside this item's blocks go into the pages first; the barrier
   // (workgroup-scope release and acquire) makes them visible to the loads below, and only
   // this workgroup reads these blocks
@@ -911,13 +948,24 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  float2* fs = sync_stats(a);
+  // the zeroing stores of this item's partial slot have completed before its statistics are
+  // published (placed here, the wait only covers the last, unused q.k^T prefetch; after the
+  // block-table loads it cost one-layer calls 0.5 us)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  SDV_VMCNT0();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  uint64_t* fs = sync_stats(a);
   // the item's statistics of each row, merged in an order that does not depend on which
   // wavefront took which block in q.k^T.  One row per wavefront (decode): lane l merges
   // blocks l, l+64, ... in order, then a fixed xor tree over the 64 lanes.  More rows
   // (verify): the wavefront owns rows wave, wave + W, ... (rpw of them) and gives each a group
   // of lpr lanes, so all its rows go through one pass (lane sl of a group merges blocks sl,
   // sl + lpr, ... in order, then a fixed xor tree inside the group).
+  auto publish_stat = [&](int row, float m, float l) {
+    uint64_t* p = fs + 2 * ((int64_t)item * 64 + row);
+    store_dev_u64(p, tagged(m, a.tag));
+    store_dev_u64(p + 1, tagged(l, a.tag));
+  };
   const int rpw = (a.R + W - 1) / W;  // <= 16: R <= 64 rows, W >= 4
   if (rpw == 1) {
     if (wave < a.R) {
@@ -935,7 +983,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       if (nbv > 8) merge_xor_low<8>(m, l);
       if (nbv > 16) merge_lanes<16>(m, l);
       if (nbv > 32) merge_lanes<32>(m, l);
-      if (lane == 0) store_dev_f2(fs + (int64_t)item * 64 + wave, make_float2(m, l));
+      if (lane == 0) publish_stat(wave, m, l);
     }
   } else {
     const int lpr = rpw <= 2 ? 32 : rpw <= 4 ? 16 : rpw <= 8 ? 8 : 4;
@@ -956,23 +1004,27 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     if (lpr > 4) merge_xor_low<4>(m, l);
     if (lpr > 8) merge_xor_low<8>(m, l);
     if (lpr > 16) merge_lanes<16>(m, l);
-    if (act && sl == 0) store_dev_f2(fs + (int64_t)item * 64 + row, make_float2(m, l));
+    if (act && sl == 0) publish_stat(row, m, l);
   }
 
   // ------------------------------------------------------------------ 2. p.V
   const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
   const float* slayer = a.v_scales + layer * a.s_ls;
-  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(sync_parts(a), (short)0, (int)kSyncPartBytes, 0x00020000);
-  const int64_t pstride = (int64_t)a.R * D;  // floats per item
   float* lparts = reinterpret_cast<float*>(smem + lay.parts);
   float2* lgs = reinterpret_cast<float2*>(smem + lay.gstats);  // per row: group (max, 1/sum)
   // the group's statistics: wavefront nt waits until all nvq items have published row tile nt, merges them
   // in a fixed order -- item slice j takes items j, j+nsl, ..., then a fixed tree -- and shares
   // (max, 1/sum) of each row through LDS, so every wavefront and workgroup of the group gets
-  // identical values.  The other wavefronts' V loads stay in flight across the barrier.
+  // identical values.  The other wavefronts' V loads stay in flight across the barrier.  An
+  // expired wait leaves (NaN, NaN): every probability, partial and output of the group is NaN.
+  // A graph-recorded call reads the poison word with its first poll: on a poisoned workspace
+  // (an earlier graph-recorded call expired, so statistics words carrying a recorded tag may be
+  // left over) the call is refused the same way -- NaN statistics, NaN outputs, counted.
   auto group_stats = [&](float (&gm)[NT], float (&ginv)[NT]) {
     if (wave < NT) {  // wavefront nt polls and merges row tile nt (all tiles at once)
-      constexpr int PB = D == 128 ? 16 : 8;  // entries in flight per lane (registers allow)
+      // entries in flight per lane: a group has at most kFusedGroupItems = 32 items and a
+      // slice at least a quarter of them
+      constexpr int PB = 8;
       // lane = (item slice, row): 16 rows x 4 slices, or 8 x 8 when the rows fit in 8 and the
       // group has more than 8 items, so that more lanes share the merges (one layer at 8K, 64
       // items: 13.3 -> 12.8 us; with 4 or 5 items the extra tree level costs more than it saves)
@@ -984,38 +1036,49 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       {
         const int nt = wave;
         const int rr = nt * 16 + rl;
-        const float2* fp = fs + (int64_t)item0 * 64 + (rr < a.R ? rr : 0);
+        const uint64_t* fp = fs + 2 * ((int64_t)item0 * 64 + (rr < a.R ? rr : 0));
+        const uint64_t ready_word = (uint64_t)a.tag << 32;  // stands in for entries past the slice
         float m = -INFINITY, l = 0.0f;
+        const uint32_t poison =
+            graph_call ? __hip_atomic_load(a.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        bool expired = false;
         for (int k0 = 0; k0 < ne_max; k0 += PB) {
-          uint64_t e[PB];
+          uint64_t em[PB], el[PB];
 #pragma unroll
-          for (int k = 0; k < PB; ++k) e[k] = k0 + k < ne ? load_dev_u64(fp + (int64_t)(sl + nsl * (k0 + k)) * 64) : 1;
+          for (int k = 0; k < PB; ++k) {
+            const uint64_t* ep = fp + (int64_t)(sl + nsl * (k0 + k)) * 128;
+            em[k] = k0 + k < ne ? load_dev_u64(ep) : ready_word;
+            el[k] = k0 + k < ne ? load_dev_u64(ep + 1) : ready_word;
+          }
           unsigned spins = 0;
           for (;;) {
             bool ready = true;
 #pragma unroll
-            for (int k = 0; k < PB; ++k) ready = ready && e[k] != 0;
+            for (int k = 0; k < PB; ++k) ready = ready && has_tag(em[k], a.tag) && has_tag(el[k], a.tag);
             if (__ballot(!ready) == 0) break;
-            if (++spins > (1u << 20)) {
-              if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (++spins >= a.spin_limit) {
+              expired = true;
               break;
             }
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-            for (int k = 0; k < PB; ++k)
-              if (e[k] == 0) e[k] = load_dev_u64(fp + (int64_t)(sl + nsl * (k0 + k)) * 64);
-          }
-#pragma unroll
-          for (int k = 0; k < PB; ++k) {
-            if (k0 + k < ne) {
-              const float2 v = __builtin_bit_cast(float2, e[k]);
-              merge_fast(m, l, v.x, v.y);
+            for (int k = 0; k < PB; ++k) {
+              const uint64_t* ep = fp + (int64_t)(sl + nsl * (k0 + k)) * 128;
+              if (!has_tag(em[k], a.tag)) em[k] = load_dev_u64(ep);
+              if (!has_tag(el[k], a.tag)) el[k] = load_dev_u64(ep + 1);
             }
           }
+#pragma unroll
+          for (int k = 0; k < PB; ++k)
+            if (k0 + k < ne) merge_fast(m, l, word_value(em[k]), word_value(el[k]));
         }
         if (narrow) merge_xor_low<8>(m, l);  // slices 2j and 2j+1 (lanes with bit 3 clear)
         merge_lanes<16>(m, l);
         merge_lanes<32>(m, l);
+        if (expired || poison != 0) {  // wave-uniform (the poll loop exits on a ballot)
+          m = l = __builtin_nanf("");
+          if (lane == 0) s_fail = 1;
+        }
         if (sl == 0 && rr < a.R) lgs[rr] = make_float2(m, 1.0f / l);
       }
     }
@@ -1203,10 +1266,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     // the ring has (first poll check 3.2 us after the publish against 1.6 us for decode; 28
     // layers at 8K: 48.8-49.5 -> 47.7-47.8 us).  Small items lose by it (one layer: +0.9
     // us): their wait is short and their ring is most of their p.V.
-#ifndef SDV_TUNE_PF_MIN
-#define SDV_TUNE_PF_MIN 32
-#endif
-    constexpr int kPollFirstMinBlocks = SDV_TUNE_PF_MIN;
+    constexpr int kPollFirstMinBlocks = 32;
     const bool poll_first = a.f_maxblk >= kPollFirstMinBlocks;  // workgroup-uniform
     if (!poll_first || wave >= NT) {  // wave-uniform
   #pragma unroll
@@ -1328,16 +1388,13 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   }
 
   // ------------------------------------------------------------------ 3. output
-  // Workgroup c < nvq of the group owns output chunks [c*per, c*per + per) (16 bytes each) and
-  // sums them over the group's items in item order.  Partial words are never 0 once written,
+  // Workgroup c < nvq of the group owns output chunks [lo, lo + w) (16 bytes each) and sums
+  // them over the group's items in item order.  Partial words are never 0 once written, and
+  // every item's slot was zeroed before that item published the statistics this workgroup took,
   // so the owner polls the data itself.  Having seen every item's chunks it knows that every
-  // workgroup of the group is past its statistics: it clears the chunks it consumed and its
-  // share of the statistics, leaving the synchronisation area zero for the next call.
-  const int n4 = a.R * D / 4;
-  const int per = (n4 + nvq - 1) / nvq;
-  const int lo = c * per, w = max(min(n4, lo + per) - lo, 0);
-  const int nown = (n4 + per - 1) / per;  // workgroups with a non-empty share
-  const int nld = w * nvq;                 // chunks this workgroup reads
+  // workgroup of the group is past its statistics: it clears its share of them, leaving the
+  // statistics area zero for the next call (the replays of a graph reuse their tag).
+  const int nld = w * nvq;  // chunks this workgroup reads
   float4* red = reinterpret_cast<float4*>(smem + lay.red);
   __syncthreads();  // LDS is reused below
   auto poll_chunks_one = [&]() {  // at most one chunk per thread
@@ -1351,8 +1408,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     for (;;) {
       const bool ready = v[0] != 0u && v[1] != 0u && v[2] != 0u && v[3] != 0u;
       if (__ballot(!ready) == 0) break;
-      if (++spins > (1u << 20)) {
-        if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (++spins >= a.spin_limit) {
+        if (lane == 0) s_fail = 1;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -1383,8 +1440,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < kOutLoads; ++r) ready = ready && v[r][0] != 0u && v[r][1] != 0u && v[r][2] != 0u && v[r][3] != 0u;
         if (__ballot(!ready) == 0) break;
-        if (++spins > (1u << 20)) {
-          if (lane == 0) __hip_atomic_fetch_add(a.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++spins >= a.spin_limit) {
+          if (lane == 0) s_fail = 1;
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -1405,6 +1462,16 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   else
     poll_chunks_many();
   __syncthreads();
+  // a wait of this workgroup expired: its outputs become NaN, the error is counted (and a
+  // graph-recorded call poisons the workspace), and nothing is cleared
+  if (s_fail) {
+    nan_slice();
+    if (tid == 0) {
+      count_sync_error(a);
+      if (graph_call) __hip_atomic_store(a.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
   // Sum over the items in a fixed order.  For 16 items or more and enough threads, in two
   // levels: thread (sg, o) adds the items of segment sg (about sqrt(nvq) of them) in order,
   // then thread o adds the segments in order; one thread per chunk would walk a dependent
@@ -1461,14 +1528,12 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     uint16_t* dst = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d;
     *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(sm.x, sm.y), pack_bf16x2(sm.z, sm.w));
   }
-  for (int e = tid; e < nld; e += NTHR) {
-    const int cc = e / w, o = e - cc * w;
-    __builtin_amdgcn_raw_buffer_store_b128((u32x4_t){0u, 0u, 0u, 0u}, prs,
-                                           (int)(((int64_t)(item0 + cc) * pstride + 4 * (lo + o)) * 4), 0, 16);
-  }
   if (c < nown) {
-    for (int e = c + tid * nown; e < nvq * a.R; e += NTHR * nown)
-      store_dev_f2(fs + (int64_t)(item0 + e / a.R) * 64 + e % a.R, make_float2(0.0f, 0.0f));
+    for (int e = c + tid * nown; e < nvq * a.R; e += NTHR * nown) {
+      uint64_t* p = fs + 2 * ((int64_t)(item0 + e / a.R) * 64 + e % a.R);
+      store_dev_u64(p, 0);
+      store_dev_u64(p + 1, 0);
+    }
   }
 }
 
@@ -1513,12 +1578,6 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   while (qb < qb_max && blocks > (int64_t)kWaves * qb * 1024) qb *= 2;
   int pb = 4;  // multiple of the 4-block pv stage
   while (pb < kWave && blocks > (int64_t)kWaves * pb * 512) pb *= 2;
-#ifdef SDV_TUNE_QK_BPW  // tuning builds only: fixed blocks per wavefront
-  qb = min(SDV_TUNE_QK_BPW, qb_max);
-#endif
-#ifdef SDV_TUNE_PV_BPW
-  pb = min((SDV_TUNE_PV_BPW + 3) / 4 * 4, kWave);
-#endif
   p->qk_bpw = qb;
   p->qk_chunk_tokens = kWaves * qb * kBlock;
   p->n_qk_chunks = (max_seq_len + p->qk_chunk_tokens - 1) / p->qk_chunk_tokens;
@@ -1566,10 +1625,7 @@ static int fused_capacity(size_t lds) {
     (void)hipGetLastError();
     return 0;
   }
-  // Decode (one row tile): one workgroup per CU, whatever the register count would allow.  A
-  // second resident workgroup only splits the CU's bandwidth between two items of the same
-  // size (measured on 28 layers at 8K: 504 workgroups 42.7-43.1 us against 224 at 39.4 us).
-  if (NT == 1) per_cu = min(per_cu, kFusedMaxPerCU);
+  per_cu = min(per_cu, fused_max_per_cu<D, NT>());
   cap = per_cu * cus;
   cache[dev][bucket].store(cap, std::memory_order_relaxed);
   return cap;
@@ -1585,15 +1641,12 @@ struct FusedShape {
 // serve the call (several query-row groups, too many groups, items too large for LDS).
 template <int D, int NT, int W>
 static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
-#ifdef SDV_TUNE_NO_FUSED  // tuning builds only: always the three-launch path
-  return false;
-#endif
   if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;
   const int G = (int)p.groups;
   const int gb = (max_seq_len + kBlock - 1) / kBlock;
-  // at most kFusedGroupItems items of at least kFusedMinBlocks blocks: a small problem (one
-  // layer) spread over every CU would spend its time in the cross-workgroup exchanges
-  const int max_items = min(min(kFusedGroupItems, gb), max(1, gb / kFusedMinBlocks));
+  // at most kFusedGroupItems items of at least one block: a small problem (one layer) spread
+  // over every CU would spend its time in the cross-workgroup exchanges
+  const int max_items = min(kFusedGroupItems, gb);
   // items whose fp32 partials fit the sync area
   const int part_cap = (int)(kSyncPartBytes / ((size_t)R * D * 4));
   constexpr int NTGN = fused_ntg(D, W), NTGW = fused_ntg_wide(D, W, NT);
@@ -1705,6 +1758,27 @@ extern "C" size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch
   return p.total;
 }
 
+// Tag of a single-launch call: unique among the process's calls (never 0; 31 bits), with
+// kTagGraph set when the stream is recording a graph (whose replays reuse the tag).
+static std::atomic<uint32_t> g_calls{0};
+static std::atomic<uint32_t> g_wait_limit{0};  // 0: kDefaultSpinLimit
+
+static uint32_t next_call_tag(hipStream_t st) {
+  uint32_t t = 0;
+  while (t == 0) t = (g_calls.fetch_add(1, std::memory_order_relaxed) + 1u) & ~kTagGraph;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess)
+    (void)hipGetLastError();
+  else if (cs == hipStreamCaptureStatusActive)
+    t |= kTagGraph;
+  return t;
+}
+
+static uint32_t wait_limit() {
+  const uint32_t v = g_wait_limit.load(std::memory_order_relaxed);
+  return v ? v : kDefaultSpinLimit;
+}
+
 // The new tokens to append before attending (sdv_paged_attention_append).
 struct AppendIn {
   const void* k_new;
@@ -1792,6 +1866,8 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.app_scale_mode = 0;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
+  a.tag = next_call_tag(st);
+  a.spin_limit = wait_limit();
   if (app) {
     const int64_t per_layer = (int64_t)batch * q_len * kv_heads * head_dim;
     if (!app->k_new || !app->v_new || !app->slot_mapping) return SDV_ERR_NULL;
@@ -1876,6 +1952,27 @@ extern "C" int sdv_attention_workspace_init(void* workspace, size_t workspace_by
   hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<uint32_t*>(workspace), kSyncBytes / 4);
   return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
+}
+
+extern "C" int sdv_attention_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* failures,
+                                              uint32_t* poisoned, void* stream) {
+  if (!workspace || !failures || !poisoned) return SDV_ERR_NULL;
+  if (!aligned(workspace, 256) || workspace_bytes < kSyncBytes) return SDV_ERR_WORKSPACE;
+  uint32_t head[2] = {0, 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(head, workspace, sizeof(head), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    (void)hipGetLastError();
+    return SDV_ERR_HIP;
+  }
+  *failures = head[0];
+  *poisoned = head[1];
+  return SDV_OK;
+}
+
+extern "C" int sdv_attention_set_wait_limit(uint32_t polls) {
+  g_wait_limit.store(polls, std::memory_order_relaxed);
+  return SDV_OK;
 }
 
 extern "C" int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,

@@ -17,17 +17,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Loads of page data that is read exactly once per call (K, V codes, V scales) carry the
 // non-temporal hint: on gfx950 streaming reads with it sustain a higher share of HBM
 // bandwidth than plain loads, and they do not displace the reused lines (scores, q).
-#ifndef SDV_STREAM_LOADS
-#define SDV_STREAM_LOADS 1
-#endif
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_stream16(const void* p) {
-#if SDV_STREAM_LOADS
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *reinterpret_cast<const uint4*>(p);
-#endif
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

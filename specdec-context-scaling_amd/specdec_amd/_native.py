@@ -34,7 +34,7 @@ PHASE_REDUCE = 4
 PHASE_ALL = 7
 
 BLOCK_SIZE = 16
-SYNC_BYTES = 10486016       # SDV_SYNC_BYTES: workspace prefix the single-launch path synchronises through
+SYNC_BYTES = 12583168       # SDV_SYNC_BYTES: workspace prefix the single-launch path synchronises through
 ABI_VERSION = 1
 
 # Every symbol include/sdv.h declares, with its ctypes signature.
@@ -49,6 +49,9 @@ SIGNATURES = {
                                               _P, _P, _P, _I32, _I64, _I64, _I64, _I32, _P, _I32, _P]),
     "sdv_attention_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "sdv_attention_workspace_init": (ctypes.c_int, [_P, _SZ, _P]),
+    "sdv_attention_workspace_status": (ctypes.c_int, [_P, _SZ, ctypes.POINTER(ctypes.c_uint32),
+                                                      ctypes.POINTER(ctypes.c_uint32), _P]),
+    "sdv_attention_set_wait_limit": (ctypes.c_int, [ctypes.c_uint32]),
     "sdv_attention_single_launch": (ctypes.c_int32, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "sdv_paged_attention": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _P,
                                            _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,

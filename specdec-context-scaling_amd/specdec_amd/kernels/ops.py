@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import os
 import weakref
 
 import torch
@@ -32,7 +33,11 @@ _SCALE_MODES = {"div": _native.SCALE_DIV, "rcp": _native.SCALE_RCP}
 _BACKENDS = ("hip", "cuda")  # "cuda" is what reference call sites pass (patch.py:107)
 
 _WORKSPACES: dict = {}
+_RETIRED: list = []  # cached workspaces replaced by larger ones (a recorded graph may still use them)
 _READY: dict = {}  # id(tensor) -> weakref of workspaces whose sync prefix is known to be zero
+# SDV_CHECK_SYNC=1: every paged_attention call reads its workspace's failure count afterwards
+# and raises SdvError when a single-launch wait expired (synchronises; a debugging aid)
+_CHECK_SYNC = os.environ.get("SDV_CHECK_SYNC", "0") not in ("", "0")
 
 
 def _fail(msg: str):
@@ -103,11 +108,18 @@ def _init_workspace(ws: torch.Tensor) -> None:
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A cached uint8 workspace of at least nbytes on (device, current stream)."""
+    """A cached uint8 workspace of at least nbytes on (device, current stream).
+
+    A cached buffer that is too small is replaced by a larger one but kept alive: a HIP graph
+    recorded with it still points at it.  Callers that record graphs should rather pass
+    their own buffer (``workspace_tensor``) and keep it for the graph's lifetime.
+    """
     dev = torch.device(device)
     key = (dev, _stream(dev))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = new_workspace(dev, max(nbytes, 1 << 20))
         _WORKSPACES[key] = ws
     return ws
@@ -121,9 +133,43 @@ def single_launch_workgroups(num_layers: int, batch: int, q_heads: int, kv_heads
                                                            max_seq_len))
 
 
+def workspace_status(ws: torch.Tensor) -> tuple[int, bool]:
+    """(failures, poisoned) of a workspace (sdv_attention_workspace_status; synchronises the
+    current stream): failures = expired waits and refused calls of the single-launch path
+    since the workspace was initialised; poisoned = graph-recorded calls are being refused
+    until reset_workspace()."""
+    fail, poison = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    _native.check(_native.load().sdv_attention_workspace_status(_p(ws), ws.numel(), ctypes.byref(fail),
+                                                                 ctypes.byref(poison), _stream(ws.device)),
+                  "sdv_attention_workspace_status")
+    return int(fail.value), bool(poison.value)
+
+
 def sync_errors(ws: torch.Tensor) -> int:
-    """Expired waits of the single-launch path recorded in a workspace (synchronises)."""
-    return int(ws[:4].view(torch.int32).item())
+    """Expired waits and refused calls of the single-launch path recorded in a workspace
+    (synchronises)."""
+    return workspace_status(ws)[0]
+
+
+def check_workspace(ws: torch.Tensor) -> None:
+    """Raise SdvError when a single-launch call on this workspace could not complete (its
+    outputs hold NaN where it failed); the reference raises every error (model_self.py:331-332)."""
+    fail, poison = workspace_status(ws)
+    if fail or poison:
+        raise SdvError(f"single-launch attention: {fail} wait(s) expired or call(s) refused on this workspace"
+                       f"{' (graph-recorded calls poisoned)' if poison else ''}; outputs of the failed calls are NaN. "
+                       f"Call ops.reset_workspace() before recording new graphs on it", _native.SDV_ERR_HIP)
+
+
+def reset_workspace(ws: torch.Tensor) -> None:
+    """Zero a workspace's synchronisation area (clears the failure count and the graph poison)."""
+    _init_workspace(ws)
+
+
+def set_wait_limit(polls: int) -> None:
+    """Bound of the single launch's cross-workgroup waits for later calls (0: the default);
+    tests use a tiny bound to drive the failure path."""
+    _native.check(_native.load().sdv_attention_set_wait_limit(int(polls)), "sdv_attention_set_wait_limit")
 
 
 @functools.lru_cache(maxsize=256)
@@ -298,12 +344,16 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
         st = lib.sdv_paged_attention_append(*args[:-1], _p(k_new), _p(v_new), _p(slots), per(v_new),
                                             _SCALE_MODES[scale_mode], args[-1])
         _native.check(st, "sdv_paged_attention_append")
+        if _CHECK_SYNC:
+            check_workspace(workspace_tensor)
         return out
     if phases == _native.PHASE_ALL:
         st = lib.sdv_paged_attention(*args)
     else:
         st = lib.sdv_paged_attention_phases(*args, int(phases))
     _native.check(st, "sdv_paged_attention")
+    if _CHECK_SYNC:
+        check_workspace(workspace_tensor)
     return out
 
 

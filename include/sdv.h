@@ -233,6 +233,30 @@ int sdv_paged_attention_append(const void* q, const void* k_pages, const void* v
                                const int32_t* slot_mapping, int64_t new_layer_stride,
                                int32_t scale_mode, void* stream);
 
+/*
+ * sdv_paged_attention without a workspace argument and without allocating: the library's own
+ * device-resident scratch array (one per GPU, SDV_NOALLOC_MAX_WORKSPACE bytes, held until the
+ * process ends) serves as the workspace.  Arguments and results as sdv_paged_attention.  Calls
+ * whose chosen path needs more than the array holds return SDV_ERR_WORKSPACE (the single
+ * launch -- decode and verify shapes that fit the device at once -- needs SDV_SYNC_BYTES;
+ * the three-launch path needs sdv_attention_workspace_size bytes).  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other threads) race,
+ * so order them on one stream.  The first call on a device takes the array's address and
+ * zeroes its synchronisation area, waiting for that to finish, so it must not be recorded
+ * into a graph (SDV_ERR_UNSUPPORTED); later calls may be.  No counterpart in the reference:
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+#define SDV_NOALLOC_MAX_WORKSPACE 33554432
+int sdv_paged_attention_noalloc(const void* q, const void* k_pages, const void* v_pages,
+                                const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                                int64_t v_layer_stride, int64_t s_layer_stride,
+                                const int32_t* block_table, int32_t max_blocks_per_seq,
+                                const int32_t* seq_lens,
+                                int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                                int32_t q_len, int32_t head_dim, int32_t max_seq_len,
+                                int32_t q_token_major, void* out, void* stream);
+
 /* Elementwise fp32 -> E4M3FN (RNE, NaN beyond 464 / for Inf and NaN), device buffers. */
 int sdv_fp8_encode(const float* in, uint8_t* out, int64_t n, void* stream);
 

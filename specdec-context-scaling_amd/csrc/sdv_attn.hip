@@ -29,6 +29,7 @@
 // supplies column l%16, both with the same 8 k-slots for lane group l/16; the result lane
 // l holds rows 4*(l/16)+i, column l%16.  Every operand below uses that mapping.
 #include <atomic>
+#include <mutex>
 
 #include "sdv_internal.h"
 
@@ -1793,7 +1794,8 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
                      const int32_t* block_table, int32_t max_blocks_per_seq, const int32_t* seq_lens,
                      int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t q_len,
                      int32_t head_dim, int32_t max_seq_len, int32_t q_token_major, void* workspace,
-                     size_t workspace_bytes, void* out, void* stream, int32_t phase_mask, const AppendIn* app) {
+                     size_t workspace_bytes, void* out, void* stream, int32_t phase_mask, const AppendIn* app,
+                     bool path_sized_ws = false) {
   if (phase_mask <= 0 || phase_mask > SDV_PHASE_ALL) return SDV_ERR_SHAPE;
   if (!q || !k_pages || !v_pages || !v_scales || !block_table || !seq_lens || !out) return SDV_ERR_NULL;
   if (head_dim != 64 && head_dim != 128) return SDV_ERR_UNSUPPORTED;
@@ -1806,7 +1808,15 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   const int64_t s_page = (int64_t)num_blocks * kv_heads * kBlock;
   if (num_layers > 1 && (k_layer_stride < k_page || v_layer_stride < k_page || s_layer_stride < s_page))
     return SDV_ERR_SHAPE;
-  if (!workspace || workspace_bytes < p.total || !aligned(workspace, 256)) return SDV_ERR_WORKSPACE;
+  // path_sized_ws: the workspace only has to hold what the chosen path touches (the
+  // synchronisation area for the single launch); otherwise sdv_attention_workspace_size bytes
+  size_t need = p.total;
+  if (path_sized_ws && phase_mask == SDV_PHASE_ALL) {
+    const int R = (q_heads / kv_heads) * q_len;
+    const int grid = head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len) : fused_grid_for<64>(p, R, max_seq_len);
+    if (grid > 0) need = kSyncBytes;
+  }
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return SDV_ERR_WORKSPACE;
   if (!aligned(q, 16) || !aligned(out, 16) || !aligned(k_pages, 16) || !aligned(v_scales, 16) ||
       !aligned(v_pages, 4) || !aligned(block_table, 4) || !aligned(seq_lens, 4))
     return SDV_ERR_ALIGN;
@@ -1952,6 +1962,68 @@ extern "C" int sdv_attention_workspace_init(void* workspace, size_t workspace_by
   hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<uint32_t*>(workspace), kSyncBytes / 4);
   return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
+}
+
+// ---------------------------------------------------------------------------- no-allocation entry point
+// Device-resident workspace for sdv_paged_attention_noalloc: one copy per GPU the library runs
+// on, held until the process ends.  Host code never passes `scratch` itself to a kernel (in
+// host code the name is only a stand-in for the symbol): each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kScratchBytes = (size_t)SDV_NOALLOC_MAX_WORKSPACE;
+static_assert(kScratchBytes >= kSyncBytes && kScratchBytes % 256 == 0, "scratch holds the synchronisation area");
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// This device's scratch address; the first call on a device takes the symbol's address and
+// zeroes its synchronisation area (a fill kernel on `st`, then waits for it), which cannot be
+// recorded into a graph.
+static int scratch_for_device(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return SDV_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      return SDV_ERR_HIP;
+    }
+    if (cs != hipStreamCaptureStatusNone) return SDV_ERR_UNSUPPORTED;
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      return SDV_ERR_HIP;
+    }
+    hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, st, static_cast<uint32_t*>(ptr), kSyncBytes / 4);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+      (void)hipGetLastError();
+      return SDV_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SDV_OK;
+}
+
+extern "C" int sdv_paged_attention_noalloc(const void* q, const void* k_pages, const void* v_pages,
+                                           const float* v_scales, int32_t num_blocks, int64_t k_layer_stride,
+                                           int64_t v_layer_stride, int64_t s_layer_stride,
+                                           const int32_t* block_table, int32_t max_blocks_per_seq,
+                                           const int32_t* seq_lens, int32_t num_layers, int32_t batch,
+                                           int32_t q_heads, int32_t kv_heads, int32_t q_len, int32_t head_dim,
+                                           int32_t max_seq_len, int32_t q_token_major, void* out, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = scratch_for_device(st, &ws);
+  if (rc != SDV_OK) return rc;
+  return attention(q, k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride, s_layer_stride,
+                   block_table, max_blocks_per_seq, seq_lens, num_layers, batch, q_heads, kv_heads, q_len, head_dim,
+                   max_seq_len, q_token_major, ws, kScratchBytes, out, stream, SDV_PHASE_ALL, nullptr,
+                   /*path_sized_ws=*/true);
 }
 
 extern "C" int sdv_attention_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* failures,

@@ -35,6 +35,7 @@ PHASE_ALL = 7
 
 BLOCK_SIZE = 16
 SYNC_BYTES = 12583168       # SDV_SYNC_BYTES: workspace prefix the single-launch path synchronises through
+NOALLOC_MAX_WORKSPACE = 33554432  # SDV_NOALLOC_MAX_WORKSPACE: the no-allocation entry point's scratch per GPU
 ABI_VERSION = 1
 
 # Every symbol include/sdv.h declares, with its ctypes signature.
@@ -62,6 +63,8 @@ SIGNATURES = {
     "sdv_paged_attention_append": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _P,
                                                   _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
                                                   _P, _SZ, _P, _P, _P, _P, _I64, _I32, _P]),
+    "sdv_paged_attention_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I64, _I64, _I64, _P, _I32, _P,
+                                                   _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P]),
     "sdv_fp8_encode": (ctypes.c_int, [_P, _P, _I64, _P]),
     "sdv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "sdv_abi_version": (ctypes.c_int, []),

@@ -1,0 +1,95 @@
+"""sdv_paged_attention_noalloc -- the entry point that allocates nothing -- through the C ABI.
+
+It runs the same kernels as sdv_paged_attention with the library's per-GPU scratch array in
+place of a caller's workspace, so its outputs must equal sdv_paged_attention's bit for bit:
+checked on two calls in a row, the second with a smaller input (the scratch keeps the first
+call's contents), and a call whose path needs more workspace than the scratch holds must be
+rejected with SDV_ERR_WORKSPACE before anything is launched.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import announce
+from specdec_amd import _native
+from specdec_amd import workloads as wl
+from specdec_amd.engine.paged_cache import PagedKVCache
+from specdec_amd.kernels import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(dev, layers, kv, d, t, seed):
+    g = wl.gen(seed, dev)
+    cache = PagedKVCache(kv, d, num_layers=layers, num_blocks=t // 16 + 3, device=dev, seed=seed, growable=False)
+    slots = None
+    for layer in range(layers):
+        k = torch.randn((t, kv, d), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((t, kv, d), generator=g, device=dev).to(torch.bfloat16)
+        slots = cache.prefill(layer, k, v, [t], slots)
+    return cache
+
+
+def _noalloc(q, cache, t, out):
+    """One sdv_paged_attention_noalloc call (q (L, 1, H, S, D) or (1, H, S, D) for one layer)."""
+    lib = _native.load()
+    layered = q.dim() == 5
+    L = q.shape[0] if layered else 1
+    B, H, S, D = q.shape[-4:]
+    kp, vp, vs = (cache.k_pages, cache.v_pages, cache.v_scales) if layered else cache.layer(0)
+    per = (lambda x: x[0].numel()) if layered else (lambda x: 0)
+    bt, sl = cache.block_table(), cache.seq_lens_tensor()
+    nb = kp.shape[-5]
+    return lib.sdv_paged_attention_noalloc(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), vs.data_ptr(), nb,
+                                           per(kp), per(vp), per(vs), bt.data_ptr(), bt.shape[1], sl.data_ptr(),
+                                           L, B, H, cache.kv_heads, S, D, t, 0, out.data_ptr(),
+                                           torch.cuda.current_stream().cuda_stream)
+
+
+def test_noalloc_matches_workspace_entry_point(cuda_device):
+    # call 1: the headline shape, 28 layers at 8K, one launch of the single-launch kernel
+    announce("noalloc: 28 layers x 12/2/128 T=8192 decode")
+    big = _cache(cuda_device, 28, 2, 128, 8192, seed=910)
+    g = wl.gen(911, cuda_device)
+    q1 = torch.randn((28, 1, 12, 1, 128), generator=g, device=cuda_device).to(torch.bfloat16)
+    out1 = torch.empty_like(q1)
+    assert _noalloc(q1, big, 8192, out1) == _native.SDV_OK
+    ref1 = ops.paged_attention(q1, big.k_pages, big.v_pages, big.v_scales, big.block_table(),
+                               big.seq_lens_tensor(), 8192)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, ref1), "noalloc call 1 differs from sdv_paged_attention"
+    # call 2, smaller: one layer, verify S=5 at T=2048 (the scratch still holds call 1's area)
+    announce("noalloc: 1 layer x 12/2/128 S=5 T=2048 verify")
+    small = _cache(cuda_device, 1, 2, 128, 2048, seed=912)
+    q2 = torch.randn((1, 12, 5, 128), generator=g, device=cuda_device).to(torch.bfloat16)
+    out2 = torch.empty_like(q2)
+    assert _noalloc(q2, small, 2048, out2) == _native.SDV_OK
+    kp, vp, vs = small.layer(0)
+    ref2 = ops.paged_attention(q2, kp, vp, vs, small.block_table(), small.seq_lens_tensor(), 2048)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref2), "noalloc call 2 differs from sdv_paged_attention"
+    # and the first shape again, bitwise as before
+    out3 = torch.empty_like(q1)
+    assert _noalloc(q1, big, 8192, out3) == _native.SDV_OK
+    torch.cuda.synchronize()
+    assert torch.equal(out3, ref1)
+
+
+def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device):
+    """A three-launch shape whose workspace exceeds the scratch: rejected on the host."""
+    announce("noalloc: oversize three-launch shape is rejected")
+    lib = _native.load()
+    h, s, t = 12, 128, 8192
+    for s in (128, 256, 512, 1024, 2048):
+        need = lib.sdv_attention_workspace_size(1, 1, h, 2, s, 128, t)
+        if lib.sdv_attention_single_launch(1, 1, h, 2, s, 128, t) == 0 and need > _native.NOALLOC_MAX_WORKSPACE:
+            break
+    else:
+        pytest.skip("every tested shape fits the scratch")
+    cache = _cache(cuda_device, 1, 2, 128, t, seed=913)
+    q = torch.zeros((1, h, s, 128), dtype=torch.bfloat16, device=cuda_device)
+    out = torch.full_like(q, 7.0)
+    assert _noalloc(q, cache, t, out) == _native.SDV_ERR_WORKSPACE
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all()), "a rejected call must not write its output"

@@ -29,6 +29,7 @@
 // supplies column l%16, both with the same 8 k-slots for lane group l/16; the result lane
 // l holds rows 4*(l/16)+i, column l%16.  Every operand below uses that mapping.
 #include <atomic>
+#include <climits>
 #include <mutex>
 
 #include "sdv_internal.h"
@@ -205,11 +206,10 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
         lsc[wave][nt * 16 + n][(j0 + u) * 4 + g] =
             make_uint2(pack_bf16x2(s4[0], s4[1]), pack_bf16x2(s4[2], s4[3]));
         if (mt != -INFINITY) {
-          // exp(x - mn) as 2^(x log2 e - mn log2 e): one FMA per exp
+          // exp(x - mn) as 2^(x log2 e - mn log2 e): one FMA per exp; the running sum's rescale
+          // as 2^((m_old - mn) log2 e), exactly 1 while the max stays
           const float mn = fmaxf(m_run[nt], mt), nml = -mn * kLog2e;
-          float l = (m_run[nt] == -INFINITY)
-                        ? 0.0f
-                        : l_run[nt] * __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[nt], kLog2e, nml));
+          float l = (m_run[nt] == -INFINITY) ? 0.0f : l_run[nt] * __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
 #pragma unroll
           for (int i = 0; i < 4; ++i) l += __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml));
           m_run[nt] = mn;
@@ -1543,6 +1543,262 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
 }
 
+// ---------------------------------------------------------------------------- prefill
+// Shapes with more query rows than one row-tile group holds (R = G*S > 64: prefill and
+// chunked-prefill blocks, model_self.py:471-504, 637-648) in two launches whose workspace holds
+// only the per-row (max, sum) -- 8 bytes per row -- instead of the O(S*T) scores:
+//   pass 1  each wavefront takes 32 rows (two MFMA row tiles) and streams the page blocks its
+//           rows can see: S^T = K Q^T on MFMA (the K page is the A operand, the rows the B
+//           operand), scores rounded to BF16 twice, offset-causal mask, online (max, sum) per
+//           lane, merged over the lane groups into (M, L) per row.
+//   pass 2  the same wavefront streams the blocks again, two at a time, recomputes the BF16
+//           scores and forms p = bf16(exp(s - M) / L) in registers.  A lane's S^T fragment
+//           (row n, tokens 4g..4g+3 of each of the two blocks) is exactly the B operand of
+//           O^T = V_hat^T P^T with those 8 tokens as its k-slots, so the A operand is the
+//           matching 4-byte words of the dimension-major V pages (one wave load covers 16
+//           dimensions x 16 tokens of a page, contiguous), dequantized in registers
+//           (bf16(fp32(code) * scale)); O^T accumulates in fp32 and leaves as BF16, four
+//           dimensions of one row per lane.
+// Rows are head-major (row r: head r / S, token r % S) as in the other kernels.  Row r sees
+// keys j <= T - S + r % S (the eager mask); T >= S is the caller's contract (the S new tokens
+// are part of the context), and a row that sees no key outputs 0.  The page ids of the
+// workgroup's blocks are staged in LDS, kPrefillWindow at a time.
+constexpr int kPrefillRows = 32;      // query rows per wavefront
+constexpr int kPrefillWaves = 4;      // wavefronts per workgroup
+constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
+
+template <int D, bool OUT>
+__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a) {
+  constexpr int KK = D / 32, DT = D / 16, NT = 2;
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  __shared__ int lpb[kPrefillWindow];
+  __shared__ int s_kend;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int kvh = blockIdx.y, zb = blockIdx.z, b = zb % a.B, layer = zb / a.B;
+  const int T = seq_len_of(a, b);
+  const int grp = zb * a.KV + kvh;
+  const int row0 = (blockIdx.x * kPrefillWaves + wave) * kPrefillRows;
+
+  // this lane's rows (row tile nt: row row0 + nt*16 + n): q operand and last visible key
+  bf16x8 qop[NT][KK];
+  int lim[NT];
+  bool rv[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int r = row0 + nt * 16 + n;
+    rv[nt] = r < a.R;
+    const int hl = rv[nt] ? r / a.S : 0, si = rv[nt] ? r % a.S : 0;
+    const uint16_t* qp = a.q + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + g * 8;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) qop[nt][kk] = rv[nt] ? load_bf16x8(qp + kk * 32) : zero_bf16x8();
+    lim[nt] = rv[nt] ? min(T - 1, T - a.S + si) : -1;
+  }
+  // blocks this wavefront streams (keys 0 .. max lim) and the smallest lim of its rows (every
+  // key up to it is seen by every row: no mask inside a block below it)
+  int kend = max(lim[0], lim[1]) + 1;
+  int kmin = min(rv[0] ? lim[0] : INT_MAX, rv[1] ? lim[1] : INT_MAX);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    kend = max(kend, __shfl_xor(kend, off));
+    kmin = min(kmin, __shfl_xor(kmin, off));
+  }
+  const int nblk = (kend + kBlock - 1) >> 4;  // wave-uniform
+  if (tid == 0) s_kend = 0;
+  __syncthreads();
+  if (lane == 0) atomicMax(&s_kend, nblk);
+  __syncthreads();
+  const int nblk_wg = s_kend;
+
+  const uint16_t* kbase = a.k_pages + layer * a.k_ls + (int64_t)lane * 8;
+  const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
+  const float* slayer = a.v_scales + layer * a.s_ls;
+  const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
+  float2* st = a.stats + (int64_t)grp * a.R;
+
+  float m_run[NT], l_run[NT], c_run[NT];   // pass 1: running max, sum and the sum's compensation
+  float nml[NT], invl[NT];      // pass 2: -M log2 e and 1/L per row
+  f32x4 acc[DT][NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = c_run[nt] = 0.0f;
+    nml[nt] = 0.0f;
+    invl[nt] = 0.0f;
+    if (OUT && rv[nt]) {
+      const float2 v = st[row0 + nt * 16 + n];
+      if (v.y > 0.0f) {
+        nml[nt] = -v.x * kLog2e;
+        invl[nt] = 1.0f / v.y;
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // A stage is two consecutive blocks u = 0, 1: K operands, page ids and, for pass 2, the V
+  // words (lane (g, n): dimension dt*16 + n, tokens 4g..4g+3) and the four scales of those tokens.
+  struct Stage {
+    bf16x8 k[2][KK];
+    uint32_t v[2][OUT ? DT : 1];
+    float4 sc[2];
+    int pb[2];
+  };
+  for (int w0 = 0; w0 < nblk_wg; w0 += kPrefillWindow) {  // workgroup-uniform
+    const int wn = min(kPrefillWindow, nblk_wg - w0);
+    __syncthreads();  // the previous window's page ids are no longer read
+    for (int j = tid; j < wn; j += 64 * kPrefillWaves) {
+      const int pb = btrow[w0 + j];
+      lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
+    }
+    __syncthreads();
+    const int jn = max(0, min(nblk - w0, wn));  // this wavefront's blocks in the window
+    // a block past jn (or invalid) reads page 0, which is always allocated; it is never used
+    auto load_stage = [&](int s2, Stage& x) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int jb = 2 * s2 + u;
+        x.pb[u] = jb < jn ? lpb[jb] : -1;
+        const int64_t page = (int64_t)max(x.pb[u], 0) * a.KV + kvh;
+        const uint16_t* kp = kbase + page * (kBlock * D);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) x.k[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + kk * 512));
+        if constexpr (OUT) {
+          const uint8_t* vp = vlayer + (page * D + n) * kBlock + 4 * g;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) x.v[u][dt] = *reinterpret_cast<const uint32_t*>(vp + dt * 16 * kBlock);
+          x.sc[u] = *reinterpret_cast<const float4*>(slayer + page * kBlock + 4 * g);
+        }
+      }
+    };
+    auto compute_stage = [&](int s2, Stage& x) {
+      const int jg0 = w0 + 2 * s2;  // global block of u = 0
+      bf16x8 pop[NT];
+      uint32_t pw[NT][4];           // packed BF16 probabilities: u = 0 in words 0-1, u = 1 in 2-3
+      // every key of the stage exists, is valid and is seen by every row: no mask
+      const bool full = 2 * s2 + 1 < jn && x.pb[0] >= 0 && x.pb[1] >= 0 && (jg0 + 2) * kBlock - 1 <= kmin;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bool have = 2 * s2 + u < jn;  // wave-uniform
+        if (!have) {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) pw[nt][2 * u] = pw[nt][2 * u + 1] = 0u;
+          continue;
+        }
+        const int t0 = (jg0 + u) * kBlock + 4 * g;
+        const bool blk_ok = x.pb[u] >= 0;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          f32x4 sacc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int kk = 0; kk < KK; ++kk) sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.k[u][kk], qop[nt][kk], sacc, 0, 0, 0);
+          float s4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = round_bf16(round_bf16(sacc[i]) * a.inv_sqrt_d);
+            s4[i] = (full || (blk_ok && t0 + i <= lim[nt])) ? v : -INFINITY;
+          }
+          if constexpr (!OUT) {
+            // Online (max, sum) over the whole context in one lane: the sum is rescaled by
+            // exp2((m_old - m_new) log2 e), which is exactly 1 while the max stays (the one-FMA
+            // form exp2(m_old log2 e - RN(m_new log2 e)) is off by the product's rounding on every
+            // block, and L drifted by ~1e-5 at T = 8192: rel-L2 7e-4 against eager), and the
+            // sum is compensated (T/4 terms go into one fp32 accumulator; the compensation is
+            // rescaled with it).
+            const float mt = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
+            if (mt != -INFINITY) {
+#pragma clang fp contract(off)
+              const float mn = fmaxf(m_run[nt], mt), nm = -mn * kLog2e;
+              const float f = (m_run[nt] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
+              float e[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nm));
+              const float x = (e[0] + e[1]) + (e[2] + e[3]);
+              const float l = l_run[nt] * f, t = l + x;
+              c_run[nt] = c_run[nt] * f + ((l >= x) ? ((l - t) + x) : ((x - t) + l));
+              l_run[nt] = t;
+              m_run[nt] = mn;
+            }
+          } else {
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml[nt])) * invl[nt];
+            pw[nt][2 * u] = pack_bf16x2(p[0], p[1]);
+            pw[nt][2 * u + 1] = pack_bf16x2(p[2], p[3]);
+          }
+        }
+      }
+      if constexpr (OUT) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[nt][0], pw[nt][1], pw[nt][2], pw[nt][3]));
+        // codes and scales of tokens that are not in the sequence (past T, invalid or absent
+        // blocks) become 0, so that no NaN pattern of an unwritten slot reaches the MFMA
+        if (!full) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int t0 = (jg0 + u) * kBlock + 4 * g;
+            const int nv = (2 * s2 + u < jn && x.pb[u] >= 0) ? min(max(T - t0, 0), 4) : 0;
+            const uint32_t mask = nv >= 4 ? 0xFFFFFFFFu : ((1u << (8 * nv)) - 1u);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) x.v[u][dt] &= mask;
+            x.sc[u].x = nv > 0 ? x.sc[u].x : 0.0f;
+            x.sc[u].y = nv > 1 ? x.sc[u].y : 0.0f;
+            x.sc[u].z = nv > 2 ? x.sc[u].z : 0.0f;
+            x.sc[u].w = nv > 3 ? x.sc[u].w : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dt], false);
+          const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dt], true);
+          const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dt], false);
+          const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dt], true);
+          const bf16x8 vop = __builtin_bit_cast(
+              bf16x8, make_uint4(pack_bf16x2(f01.x * x.sc[0].x, f01.y * x.sc[0].y),
+                                 pack_bf16x2(f23.x * x.sc[0].z, f23.y * x.sc[0].w),
+                                 pack_bf16x2(f45.x * x.sc[1].x, f45.y * x.sc[1].y),
+                                 pack_bf16x2(f67.x * x.sc[1].z, f67.y * x.sc[1].w)));
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dt][nt], 0, 0, 0);
+        }
+      }
+    };
+    // two stages in flight: one exit, at the loop head, and unconditional reloads (see the
+    // decode kernel: a break between the halves makes the compiler wait for every load)
+    const int nst = (jn + 1) >> 1;
+    Stage sa, sb;
+    load_stage(0, sa);
+    for (int s2 = 0; s2 < nst; s2 += 2) {
+      load_stage(s2 + 1, sb);
+      compute_stage(s2, sa);
+      load_stage(s2 + 2, sa);
+      if (s2 + 1 < nst) compute_stage(s2 + 1, sb);  // wave-uniform
+    }
+  }
+
+  if constexpr (!OUT) {
+    // (max, sum) of each row over the four lane groups, in a fixed order
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float m = m_run[nt], l = l_run[nt] + c_run[nt];
+      merge_lanes<16>(m, l);
+      merge_lanes<32>(m, l);
+      if (g == 0 && rv[nt]) st[row0 + nt * 16 + n] = make_float2(m, l);
+    }
+  } else {
+    // lane (g, n) holds O[row nt*16 + n][dims dt*16 + 4g .. +3]
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (!rv[nt]) continue;
+      const int r = row0 + nt * 16 + n, hl = r / a.S, si = r % a.S;
+      uint16_t* op = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<uint2*>(op + dt * 16) =
+            make_uint2(pack_bf16x2(acc[dt][nt][0], acc[dt][nt][1]), pack_bf16x2(acc[dt][nt][2], acc[dt][nt][3]));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------- planning
 struct Plan {
   int NT, n_row_groups, rpad;
@@ -1588,6 +1844,12 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->score_stride = max(p->n_qk_chunks * p->qk_chunk_tokens, p->n_pv_chunks * p->pv_chunk_tokens);
   const int64_t groups = (int64_t)L * B * KV;
   p->groups = groups;
+  if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) only
+    p->off_scores = p->off_partial = kSyncBytes;
+    p->off_stats = kSyncBytes;
+    p->total = kSyncBytes + round_up((size_t)(groups * R * 8), 256);
+    return true;
+  }
   // the sync area [0, kSyncBytes) is shared by both layouts and only the fused kernel uses it
   const size_t scores = round_up((size_t)(groups * R * p->score_stride * 2), 256);
   const size_t stats = round_up((size_t)(groups * p->n_qk_chunks * p->rpad * 8), 256);
@@ -1726,6 +1988,12 @@ static void launch_qk_pv(const AttnArgs& a, const Plan& p, int zdim, hipStream_t
 
 template <int D>
 static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
+  if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
+    const dim3 grid((unsigned)((a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves)), a.KV, zdim);
+    if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid, dim3(64 * kPrefillWaves), 0, st, a);
+    if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid, dim3(64 * kPrefillWaves), 0, st, a);
+    return;
+  }
   if (phases == SDV_PHASE_ALL) {
     bool done = false;
     switch (p.NT) {

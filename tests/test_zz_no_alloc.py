@@ -77,18 +77,23 @@ def test_noalloc_matches_workspace_entry_point(cuda_device):
 
 
 def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device):
-    """A three-launch shape whose workspace exceeds the scratch: rejected on the host."""
+    """A three-launch shape (more (layer, sequence, KV head) groups than the device holds at
+    once) whose workspace exceeds the scratch: rejected on the host, nothing written."""
     announce("noalloc: oversize three-launch shape is rejected")
     lib = _native.load()
-    h, s, t = 12, 128, 8192
-    for s in (128, 256, 512, 1024, 2048):
-        need = lib.sdv_attention_workspace_size(1, 1, h, 2, s, 128, t)
-        if lib.sdv_attention_single_launch(1, 1, h, 2, s, 128, t) == 0 and need > _native.NOALLOC_MAX_WORKSPACE:
+    h, kv, d = 12, 2, 128
+    for L, B, t in ((8, 32, 2048), (28, 32, 2048), (8, 64, 4096)):
+        need = lib.sdv_attention_workspace_size(L, B, h, kv, 1, d, t)
+        if lib.sdv_attention_single_launch(L, B, h, kv, 1, d, t) == 0 and need > _native.NOALLOC_MAX_WORKSPACE:
             break
     else:
-        pytest.skip("every tested shape fits the scratch")
-    cache = _cache(cuda_device, 1, 2, 128, t, seed=913)
-    q = torch.zeros((1, h, s, 128), dtype=torch.bfloat16, device=cuda_device)
+        pytest.fail("no tested shape needs more workspace than the scratch holds")
+    cache = PagedKVCache(kv, d, num_layers=L, batch=B, num_blocks=B * (t // 16) + 1, device=cuda_device,
+                         growable=False)
+    for b in range(B):
+        cache.reserve(b, t)
+        cache.set_length(b, t)
+    q = torch.zeros((L, B, h, 1, d), dtype=torch.bfloat16, device=cuda_device)
     out = torch.full_like(q, 7.0)
     assert _noalloc(q, cache, t, out) == _native.SDV_ERR_WORKSPACE
     torch.cuda.synchronize()

@@ -89,27 +89,29 @@ def build_replicas(torch, dev, n, scattered=True):
 def time_steps(torch, step, steps, warmup, nrep):
     """Average ms per step of step(i) for i = 0..steps-1 (replica i % nrep).
 
-    The steps are captured into one HIP graph of 16 steps (cycling through the cache replicas)
-    that is replayed, so the timed region holds only GPU work: a Python call costs ~20 us of host
-    time, more than some of the kernels being timed.  HIP events bracket the replays on
-    torch's current stream, the stream the library launches on.
+    Exactly `warmup` steps, then exactly `steps` steps, each set captured into one HIP graph
+    (cycling through the cache replicas) and replayed once, so the timed region holds only GPU
+    work: a Python call costs ~20 us of host time, more than some of the kernels being timed.
+    HIP events bracket the timed replay on torch's current stream, the stream the library
+    launches on.
     """
-    per_graph = nrep * max(1, 16 // nrep)  # steps per graph, cycling through the replicas
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(per_graph):
-            step(i % nrep)
-    reps = max(1, -(-steps // per_graph))
-    for _ in range(max(1, -(-warmup // per_graph))):
-        graph.replay()
+    def capture(n):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n):
+                step(i % nrep)
+        return graph
+
+    if warmup > 0:
+        capture(warmup).replay()
+    timed = capture(steps)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        graph.replay()
+    timed.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / (reps * per_graph)
+    return e0.elapsed_time(e1) / steps
 
 
 def main():
@@ -359,6 +361,14 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
     del creps
     torch.cuda.empty_cache()
 
+    # row f3: the reference's prefill chunk (2048 query rows over 8192 keys), target and draft
+    out["f3_prefill_chunk_target_2048x8192"] = prefill_row(torch, dev, 12, 2, 128, 2048, 8192,
+                                                           ref={"cudnn_sdpa_ms": 4.56, "cudnn_sdpa_transient_MiB": 74.1,
+                                                                "eager_ms": 34.01, "eager_transient_MiB": 1998.1})
+    out["f3_prefill_chunk_draft_2048x8192"] = prefill_row(torch, dev, 14, 2, 64, 2048, 8192,
+                                                          ref={"cudnn_sdpa_ms": 4.12, "cudnn_sdpa_transient_MiB": 59.4,
+                                                               "eager_ms": 38.54, "eager_transient_MiB": 2288.4})
+
     # config 1: fused quantize + append of a 2048-token chunk into 28 layers (V only, and with K)
     v1s, slots1, k1s, pages1 = [], None, [], []
     for r in range(4):
@@ -383,6 +393,54 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
         _progress("cpu rows")
         out["cpu"] = cpu_rows(budget_s=2.0)
     return out
+
+
+def prefill_row(torch, dev, h, kv, d, s, t, ref, nrep=2):
+    """One layer's prefill-chunk attention: s query rows (the chunk's new tokens, already in the
+    pages) over t keys with the offset-causal mask, q in the projection layout (B, S, H, D) as
+    the engine pack passes it.  Reports time, MFMA rate and the call's transient device memory
+    (workspace + output) beside the reference's measurement on its RTX 4060 Laptop
+    (docs/data_ledger.md:1145-1152)."""
+    from specdec_amd.engine.paged_cache import PagedKVCache
+    from specdec_amd.kernels import ops
+
+    _progress(f"prefill {h}/{kv}/{d} {s}x{t}")
+    g = torch.Generator(device=dev)
+    g.manual_seed(901)
+    reps = []
+    for r in range(nrep):
+        c = PagedKVCache(kv, d, num_blocks=t // 16 + 8, device=dev, seed=902 + r, growable=False)
+        c.prefill(0, torch.randn((t, kv, d), generator=g, device=dev).to(torch.bfloat16),
+                  torch.randn((t, kv, d), generator=g, device=dev).to(torch.bfloat16), [t])
+        q = torch.randn((1, s, h, d), generator=g, device=dev).to(torch.bfloat16)
+        reps.append((c, q, torch.empty_like(q), c.block_table(), c.seq_lens_tensor()))
+    nbytes = ops.attention_workspace_bytes(1, 1, h, kv, s, d, t)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    ws = ops.new_workspace(dev, nbytes)
+    c0, q0, _, bt0, sl0 = reps[0]
+    kp, vp, vs = c0.layer(0)
+    o = ops.paged_attention(q0, kp, vp, vs, bt0, sl0, t, q_token_major=True, workspace_tensor=ws)
+    torch.cuda.synchronize()
+    transient = torch.cuda.max_memory_allocated(dev) - base
+    del o
+
+    def call(r):
+        c, q, out, bt, sl = reps[r]
+        kp, vp, vs = c.layer(0)
+        ops.paged_attention(q, kp, vp, vs, bt, sl, t, q_token_major=True, out=out, workspace_tensor=ws)
+
+    us = time_steps(torch, call, 16, 4, nrep) * 1e3
+    keys = s * (t - s) + s * (s + 1) // 2          # visible (row token, key) pairs per head
+    flops = 4 * h * keys * d                         # q.k^T and p.V, as the eager path computes them
+    executed = 6 * h * keys * d                      # pass 1 recomputes q.k^T
+    return {"q_heads": h, "kv_heads": kv, "head_dim": d, "q_rows": s, "keys": t, "us_per_call": round(us, 1),
+            "launches": 2, "workspace_MiB": round(nbytes / 2 ** 20, 2),
+            "transient_MiB_workspace_plus_output": round(transient / 2 ** 20, 2),
+            "TFLOPs_algorithmic": round(flops / (us * 1e-6) / 1e12, 1),
+            "TFLOPs_executed": round(executed / (us * 1e-6) / 1e12, 1),
+            "reference_rtx4060": ref}
 
 
 def chain_row(torch, dev, reps, layers, h, kv, d, T, s, steps, fused=False):

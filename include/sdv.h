@@ -166,8 +166,10 @@ int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch, int32_t q
  * q, out: bf16, per layer [batch][q_heads][q_len][head_dim] (q_token_major = 0, the
  *         reference op's (B,H,S,D)) or [batch][q_len][q_heads][head_dim] (q_token_major = 1,
  *         the projection layout); layers are batch*q_heads*q_len*head_dim elements apart.
- * seq_lens: int32 [batch] context length T_b including the q_len new tokens (1..max_seq_len;
- *           the kernels clamp T_b to [0, max_seq_len], so no value can read out of bounds).
+ * seq_lens: int32 [batch] context length T_b including the q_len new tokens (q_len..max_seq_len;
+ *           the kernels clamp T_b to [0, max_seq_len], so no value can read out of bounds), or
+ *           NULL: every sequence has max_seq_len tokens (a call that a HIP graph records then
+ *           needs no lengths in device memory).
  * block_table: int32 [batch][max_blocks_per_seq], max_blocks_per_seq >= ceil(max_seq_len/16);
  *           an entry outside [0, num_blocks) is never dereferenced: its tokens are masked.
  * Row i of the q_len-row block attends to keys j <= T_b - q_len + i (model_self.py:755-764).
@@ -213,8 +215,12 @@ int sdv_paged_attention_phases(const void* q, const void* k_pages, const void* v
  * over the context that includes them, in one call: the same bytes in the pages and the same
  * output as the two calls in that order.  k_new/v_new: bf16 [num_layers][batch*q_len][kv_heads]
  * [head_dim] (layers new_layer_stride elements apart), token b*q_len + i at position
- * seq_lens[b] - q_len + i, slot_mapping int32 [batch*q_len] (negative = skip), scale_mode as
- * for sdv_quant_append.  On the single-launch path each workgroup writes the new tokens that
+ * seq_lens[b] - q_len + i, scale_mode as for sdv_quant_append.  slot_mapping: int32
+ * [batch*q_len] (negative = skip), each the block-table slot of its position
+ * (block_table[b][pos/16]*16 + pos%16: on the single launch the workgroup that streams a page
+ * block writes its new tokens, so a slot elsewhere would race with another workgroup's reads),
+ * or NULL: the slots are taken from the block table on the device (a call that a HIP graph
+ * records then needs no host-built slot array).  On the single-launch path each workgroup writes the new tokens that
  * fall in its own page blocks before reading them, so the append costs no launch of its own;
  * otherwise the append kernel runs first on the same stream.  No counterpart in the reference:
  * its layer forward quantizes and concatenates V (model_self.py:697-706, 778-800) and then

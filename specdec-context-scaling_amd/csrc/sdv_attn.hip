@@ -82,7 +82,7 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
 __device__ __forceinline__ bf16x8 zero_bf16x8() { return __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0)); }
 
 __device__ __forceinline__ int seq_len_of(const AttnArgs& a, int b) {
-  return min(max(a.seq_lens[b], 0), a.max_seq_len);
+  return a.seq_lens ? min(max(a.seq_lens[b], 0), a.max_seq_len) : a.max_seq_len;
 }
 
 // exp(x) as 2^(x * log2 e) on v_exp_f32.  The rounding of x * log2 e costs at most
@@ -569,7 +569,8 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
   float* sp = const_cast<float*>(a.v_scales) + layer * a.s_ls;
   for (int pos = p_lo + wave; pos < p_hi; pos += W) {  // wave-uniform
     const int row = b * a.S + (pos - first);
-    const int slot = a.app_slots[row];
+    const int slot = a.app_slots ? a.app_slots[row]
+                                 : table_slot(a.block_table + (int64_t)b * a.max_blocks, a.max_blocks, a.num_blocks, pos);
     if (slot < 0 || (int64_t)slot >= n_slots) continue;
     const int64_t in = layer * a.app_ls + ((int64_t)row * a.KV + kvh) * D + 8 * p;
     const uint4 vw = *reinterpret_cast<const uint4*>(a.app_v + in);
@@ -2065,7 +2066,7 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
                      size_t workspace_bytes, void* out, void* stream, int32_t phase_mask, const AppendIn* app,
                      bool path_sized_ws = false) {
   if (phase_mask <= 0 || phase_mask > SDV_PHASE_ALL) return SDV_ERR_SHAPE;
-  if (!q || !k_pages || !v_pages || !v_scales || !block_table || !seq_lens || !out) return SDV_ERR_NULL;
+  if (!q || !k_pages || !v_pages || !v_scales || !block_table || !out) return SDV_ERR_NULL;
   if (head_dim != 64 && head_dim != 128) return SDV_ERR_UNSUPPORTED;
   if (num_blocks <= 0 || max_blocks_per_seq <= 0) return SDV_ERR_SHAPE;
   if (q_token_major != 0 && q_token_major != 1) return SDV_ERR_SHAPE;
@@ -2148,7 +2149,7 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.spin_limit = wait_limit();
   if (app) {
     const int64_t per_layer = (int64_t)batch * q_len * kv_heads * head_dim;
-    if (!app->k_new || !app->v_new || !app->slot_mapping) return SDV_ERR_NULL;
+    if (!app->k_new || !app->v_new) return SDV_ERR_NULL;
     if (app->scale_mode != SDV_SCALE_DIV && app->scale_mode != SDV_SCALE_RCP) return SDV_ERR_UNSUPPORTED;
     if (num_layers > 1 && app->layer_stride < per_layer) return SDV_ERR_SHAPE;
     if (!aligned(app->k_new, 16) || !aligned(app->v_new, 16) || !aligned(app->slot_mapping, 4) ||
@@ -2162,12 +2163,19 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
       a.app_slots = app->slot_mapping;
       a.app_ls = num_layers > 1 ? app->layer_stride : 0;
       a.app_scale_mode = app->scale_mode;
-    } else {  // three launches: the append kernel first, on the same stream
+    } else if (app->slot_mapping) {  // other paths: the append kernel first, on the same stream
       const int st_app = sdv_quant_append(app->v_new, app->k_new, app->slot_mapping, batch * q_len, kv_heads,
                                           head_dim, head_dim, num_layers, app->layer_stride,
                                           const_cast<void*>(k_pages), const_cast<void*>(v_pages),
                                           const_cast<float*>(v_scales), num_blocks, k_layer_stride,
                                           v_layer_stride, s_layer_stride, app->scale_mode, stream);
+      if (st_app != SDV_OK) return st_app;
+    } else {  // the same, with the slots taken from the block table
+      const SlotTable table{block_table, max_blocks_per_seq, seq_lens, q_len, max_seq_len};
+      const int st_app = quant_append_table(app->v_new, app->k_new, table, batch * q_len, kv_heads, head_dim,
+                                            num_layers, app->layer_stride, const_cast<void*>(k_pages),
+                                            const_cast<void*>(v_pages), const_cast<float*>(v_scales), num_blocks,
+                                            k_layer_stride, v_layer_stride, s_layer_stride, app->scale_mode, stream);
       if (st_app != SDV_OK) return st_app;
     }
   }

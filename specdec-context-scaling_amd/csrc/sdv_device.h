@@ -131,6 +131,15 @@ __device__ __forceinline__ void token_scale(uint32_t ab, int scale_mode, float& 
   fast = ab == 0 || (ab >= kFastMinAmaxBits && ab < 0x7F800000u);
 }
 
+// ---------------------------------------------------------------- page slots
+// Slot (block * 16 + offset) of position `pos` of a sequence, through its block-table row;
+// -1 when the position lies past the row or its block id is not a valid page.
+__device__ __forceinline__ int table_slot(const int32_t* bt_row, int max_blocks, int num_blocks, int pos) {
+  if (pos < 0 || (pos >> 4) >= max_blocks) return -1;
+  const int pb = bt_row[pos >> 4];
+  return (pb >= 0 && pb < num_blocks) ? pb * kBlock + (pos & (kBlock - 1)) : -1;
+}
+
 // ---------------------------------------------------------------- wave reductions
 // DPP row rotate (within each 16-lane row).
 template <int N>

@@ -46,7 +46,17 @@ struct QuantArgs {
   uint8_t* v_pages;
   float* v_scales;
   int64_t k_ls, v_ls, s_ls;
+  SlotTable table;  // used when slots == nullptr
 };
+
+// slot of input row `row`: from the caller's mapping, or through the block table
+__device__ __forceinline__ int row_slot(const QuantArgs& a, int row) {
+  if (a.slots) return a.slots[row];
+  const int b = row / a.table.q_len, i = row - b * a.table.q_len;
+  const int T = a.table.seq_lens ? min(max(a.table.seq_lens[b], 0), a.table.max_seq_len) : a.table.max_seq_len;
+  return table_slot(a.table.block_table + (int64_t)b * a.table.max_blocks, a.table.max_blocks, a.num_blocks,
+                    T - a.table.q_len + i);
+}
 
 constexpr int kQuantWaves = 4;  // wavefronts (16-token tiles) per workgroup
 
@@ -90,8 +100,8 @@ __global__ __launch_bounds__(64 * kQuantWaves) void quant_append_kernel(QuantArg
   int slot[J], kslot[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    slot[j] = a.slots[t0 + min(r * J + j, nt - 1)];
-    if (WITH_K) kslot[j] = a.slots[t0 + min(j * RPW + r, nt - 1)];
+    slot[j] = row_slot(a, t0 + min(r * J + j, nt - 1));
+    if (WITH_K) kslot[j] = row_slot(a, t0 + min(j * RPW + r, nt - 1));
   }
   // rows past the end of the input re-read the last token (skipped below): no branches
   // around the loads, so that none of them has to land before the slots are used
@@ -211,8 +221,8 @@ static int quant_append(const void* v_new, const void* k_new, const int32_t* slo
                         int64_t in_layer_stride, void* k_pages, void* v_pages, float* v_scales,
                         int32_t num_blocks, int64_t k_layer_stride, int64_t v_layer_stride,
                         int64_t s_layer_stride, int32_t scale_mode, const int32_t* tiles, int32_t n_tiles,
-                        void* stream) {
-  if (!v_new || !slot_mapping || !v_pages || !v_scales) return SDV_ERR_NULL;
+                        void* stream, const SlotTable* table = nullptr) {
+  if (!v_new || !(slot_mapping || table) || !v_pages || !v_scales) return SDV_ERR_NULL;
   if (k_new && !k_pages) return SDV_ERR_NULL;
   if (n_tokens < 0 || kv_heads <= 0 || num_layers <= 0 || num_blocks <= 0) return SDV_ERR_SHAPE;
   if (kv_heads > 65535 || num_layers > 65535) return SDV_ERR_SHAPE;
@@ -252,6 +262,8 @@ static int quant_append(const void* v_new, const void* k_new, const int32_t* slo
 
   a.tiles = tiles;
   a.n_tiles = n_tiles;
+  a.table = table ? *table : SlotTable{nullptr, 0, nullptr, 1, 0};
+  if (!slot_mapping && (!a.table.block_table || a.table.q_len <= 0 || a.table.max_blocks <= 0)) return SDV_ERR_NULL;
 
   const int64_t n_waves = tiles ? n_tiles : (n_tokens + kBlock - 1) / kBlock;
   if (n_waves == 0) return SDV_OK;
@@ -304,4 +316,14 @@ extern "C" int sdv_quant_append_tiles(const void* v_new, const void* k_new, cons
   return quant_append(v_new, k_new, slot_mapping, n_tokens, kv_heads, head_dim, group_size, num_layers,
                       in_layer_stride, k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride,
                       s_layer_stride, scale_mode, tile_starts, n_tiles, stream);
+}
+
+int sdv::quant_append_table(const void* v_new, const void* k_new, const SlotTable& table, int32_t n_tokens,
+                            int32_t kv_heads, int32_t head_dim, int32_t num_layers, int64_t in_layer_stride,
+                            void* k_pages, void* v_pages, float* v_scales, int32_t num_blocks,
+                            int64_t k_layer_stride, int64_t v_layer_stride, int64_t s_layer_stride,
+                            int32_t scale_mode, void* stream) {
+  return quant_append(v_new, k_new, nullptr, n_tokens, kv_heads, head_dim, head_dim, num_layers, in_layer_stride,
+                      k_pages, v_pages, v_scales, num_blocks, k_layer_stride, v_layer_stride, s_layer_stride,
+                      scale_mode, nullptr, 0, stream, &table);
 }

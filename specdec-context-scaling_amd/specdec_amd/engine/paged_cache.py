@@ -15,6 +15,13 @@ layer).  The allocator hands out blocks from a free list; with ``seed`` the free
 seeded permutation, which scatters a sequence's blocks the way a long-running server's
 fragmented pool does.  When the pool runs out it doubles (new page tensors, one copy).
 
+Recording into a HIP graph: ``append_attend`` takes each new token's slot from the block
+table on the device and, with equal lengths, passes no length array, and the pool owns its
+attention workspace, so a decode or verify step copies nothing from the host and allocates
+nothing.  What it cannot do inside a recording -- add blocks (a new block table is copied
+from the host), grow the pool (new page tensors), grow the workspace -- raises instead;
+``reserve_all`` and ``workspace`` before recording make room.
+
 Ownership rule (the reference's trim returns views and its appends build new tensors, so an
 untrimmed handle keeps its data; here appends write pages in place): after
 ``trim``/``set_length`` to n tokens, the next append overwrites slots n.. of that sequence,
@@ -27,9 +34,20 @@ import random
 
 import torch
 
+from .._native import SdvError
 from ..kernels import ops
 
 BLOCK = ops.BLOCK
+
+
+def _recording(device: torch.device) -> bool:
+    return device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
+def _no_recording(device: torch.device, what: str) -> None:
+    if _recording(device):
+        raise SdvError(f"{what} while a HIP graph is being recorded; reserve the tokens (reserve_all) and size the "
+                       f"workspace before recording")
 
 
 class BlockAllocator:
@@ -80,6 +98,8 @@ class PagedKVCache:
         self.lengths: list[int] = [0] * batch
         self._bt = None
         self._tiles = None  # (lengths, device tile table) of the last prefill
+        self._ws = None     # attention workspace owned by the pool
+        self._retired = []  # replaced workspaces, kept alive for graphs that recorded them
 
     # ------------------------------------------------------------------ storage
     def _new_pages(self, nb: int):
@@ -90,6 +110,7 @@ class PagedKVCache:
         return k, v, s
 
     def _grow(self, min_blocks: int) -> None:
+        _no_recording(self.device, "the page pool would grow")
         old = self.alloc.num_blocks
         new = max(min_blocks, 2 * old)
         k, v, s = self._new_pages(new)
@@ -109,12 +130,30 @@ class PagedKVCache:
         need = -(-n_tokens // BLOCK) - len(self.blocks[seq])
         if need <= 0:
             return
+        _no_recording(self.device, f"sequence {seq} needs {need} more page blocks")
         if need > len(self.alloc.free):
             if not self.growable:
                 raise RuntimeError(f"block pool exhausted ({self.alloc.num_blocks} blocks) and growable=False")
             self._grow(self.alloc.num_blocks + need)
         self.blocks[seq].extend(self.alloc.alloc(need))
         self._bt = None
+
+    def reserve_all(self, n_tokens: int) -> None:
+        """Blocks for the first n_tokens positions of every sequence, and the device block table
+        (before recording a graph that appends up to n_tokens)."""
+        for b in range(self.batch):
+            self.reserve(b, n_tokens)
+        self.block_table()
+
+    def workspace(self, nbytes: int) -> torch.Tensor:
+        """The pool's attention workspace, at least nbytes (a larger one replaces it; the old one is
+        kept alive, since a recorded graph may use it)."""
+        if self._ws is None or self._ws.numel() < nbytes:
+            _no_recording(self.device, f"the attention workspace would grow to {nbytes} bytes")
+            if self._ws is not None:
+                self._retired.append(self._ws)
+            self._ws = ops.new_workspace(self.device, nbytes)
+        return self._ws
 
     def set_length(self, seq: int, n: int) -> None:
         if n < 0 or n > len(self.blocks[seq]) * BLOCK:
@@ -133,6 +172,7 @@ class PagedKVCache:
     def block_table(self) -> torch.Tensor:
         """int32 (batch, max_blocks) on the device; unused entries are -1 (never read)."""
         if self._bt is None:
+            _no_recording(self.device, "the block table would be rebuilt")
             mb = self.max_blocks()
             rows = [b + [-1] * (mb - len(b)) for b in self.blocks]
             self._bt = torch.tensor(rows, dtype=torch.int32).to(self.device)
@@ -169,19 +209,26 @@ class PagedKVCache:
                       out: torch.Tensor | None = None) -> torch.Tensor:
         """append(layer, k_new, v_new, starts) then attend(layer, q) in one call
         (sdv_paged_attention_append): the same pages and output, one launch on the single-launch
-        path.  k_new/v_new BF16 (B, S, KV, D); q (B, H, S, D) (or (B, S, H, D))."""
+        path.  k_new/v_new BF16 (B, S, KV, D); q (B, H, S, D) (or (B, S, H, D)).
+
+        Each new token's slot comes from the block table on the device; with equal lengths no
+        length array is passed either, and the workspace is the pool's own: such a call copies
+        nothing from the host and can be recorded into a HIP graph."""
         B, S = k_new.shape[0], k_new.shape[1]
         starts = list(self.lengths) if starts is None else list(starts)
         for b in range(B):
             self.reserve(b, starts[b] + S)
-        slots = self.slot_mapping(starts, S)
         for b in range(B):
             self.lengths[b] = starts[b] + S
         kp, vp, vs = self.layer(layer)
         shp = (B * S, self.kv_heads, self.head_dim)
-        return ops.paged_attention(q, kp, vp, vs, self.block_table(), self.seq_lens_tensor(), max(self.lengths),
-                                   q_token_major=q_token_major, out=out,
-                                   append=(k_new.reshape(shp), v_new.reshape(shp), slots),
+        tmax = max(self.lengths)
+        uniform = all(n == tmax for n in self.lengths)
+        H = q.shape[2] if q_token_major else q.shape[1]
+        ws = self.workspace(ops.attention_workspace_bytes(1, B, H, self.kv_heads, S, self.head_dim, tmax))
+        return ops.paged_attention(q, kp, vp, vs, self.block_table(), None if uniform else self.seq_lens_tensor(),
+                                   tmax, q_token_major=q_token_major, out=out, workspace_tensor=ws,
+                                   append=(k_new.reshape(shp), v_new.reshape(shp), None),
                                    scale_mode=self.scale_mode)
 
     def varlen_slots(self, lengths: list[int]) -> torch.Tensor:

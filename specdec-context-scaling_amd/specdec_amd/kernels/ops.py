@@ -272,12 +272,15 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
     q: BF16 (B, H, S, D) (or (B, S, H, D) with q_token_major=True); a leading layer dimension
     (L, ...) processes L layers in one launch with layered pages (L, num_blocks, ...).
     block_table int32 (B, max_blocks); seq_lens int32 (B,) = context length including the S
-    new tokens, each <= max_seq_len.  Returns out shaped like q (BF16).
+    new tokens, each <= max_seq_len, or None: every sequence has max_seq_len tokens (nothing
+    to copy to the device, so the call can be recorded into a HIP graph).  Returns out shaped
+    like q (BF16).
     ``phases`` (profiling) runs a subset of the three launches; see sdv_paged_attention_phases.
     ``append`` = (k_new, v_new, slot_mapping): first write the S new tokens of every sequence
     into the pages (as quant_append with ``scale_mode`` would; k_new/v_new BF16 (B*S, KV, D),
     or (L, B*S, KV, D) with layers, token b*S + i at position seq_lens[b] - S + i), in the same
-    call (sdv_paged_attention_append).
+    call (sdv_paged_attention_append); slot_mapping None takes each token's slot from the block
+    table on the device.
     """
     lib = _native.load()
     _need(q, "q", (torch.bfloat16,), ndim=(4, 5))
@@ -287,7 +290,8 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
     _need(v_pages, "v_pages", (torch.uint8, torch.float8_e4m3fn), dev)
     _need(v_scales, "v_scales", (torch.float32,), dev)
     _need(block_table, "block_table", (torch.int32,), dev, ndim=(2,))
-    _need(seq_lens, "seq_lens", (torch.int32,), dev, ndim=(1,))
+    if seq_lens is not None:
+        _need(seq_lens, "seq_lens", (torch.int32,), dev, ndim=(1,))
     nb, kv, d = _pages_dims(k_pages, v_pages, v_scales, layered)
     L = q.shape[0] if layered else 1
     if layered and k_pages.shape[0] != L:
@@ -298,8 +302,9 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
         B, H, S, Dq = q.shape[-4:]
     if Dq != d or H % kv:
         _fail(f"q {tuple(q.shape)} does not match pages (KV={kv}, D={d})")
-    if block_table.shape[0] != B or seq_lens.shape[0] != B:
-        _fail(f"block_table {tuple(block_table.shape)} / seq_lens {tuple(seq_lens.shape)} need batch {B}")
+    if block_table.shape[0] != B or (seq_lens is not None and seq_lens.shape[0] != B):
+        _fail(f"block_table {tuple(block_table.shape)} / seq_lens "
+              f"{None if seq_lens is None else tuple(seq_lens.shape)} need batch {B}")
     max_seq_len = int(max_seq_len)
     if max_seq_len <= 0 or block_table.shape[1] * BLOCK < max_seq_len:
         _fail(f"max_seq_len {max_seq_len} must be in [1, 16 * max_blocks = {block_table.shape[1] * BLOCK}]")
@@ -334,9 +339,10 @@ def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tenso
             _need(t, name, (torch.bfloat16,), dev)
             if tuple(t.shape) != want:
                 _fail(f"{name} {tuple(t.shape)} != {want}")
-        _need(slots, "slot_mapping", (torch.int32,), dev, ndim=(1,))
-        if slots.shape[0] != B * S:
-            _fail(f"slot_mapping {tuple(slots.shape)} needs {B * S} entries")
+        if slots is not None:
+            _need(slots, "slot_mapping", (torch.int32,), dev, ndim=(1,))
+            if slots.shape[0] != B * S:
+                _fail(f"slot_mapping {tuple(slots.shape)} needs {B * S} entries")
         if k_new.data_ptr() % 16:
             k_new = k_new.clone()
         if v_new.data_ptr() % 16:

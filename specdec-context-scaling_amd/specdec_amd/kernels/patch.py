@@ -102,6 +102,20 @@ def enable_fp8v(model) -> None:
         layer.self_attn.kv_format = "v_fp8"
 
 
+def reserve(cache_list, n_tokens: int) -> None:
+    """Page blocks (and the device block tables and workspaces) for n_tokens positions in every
+    layer of an engine cache, so that steps up to that length can be recorded into a HIP graph:
+    a recorded step then copies nothing from the host and allocates nothing (the reference's
+    graph experiments record the draft chain and the verify block at a fixed history length,
+    experiments/cuda_graph_local/draft_graph.py, verify_graph.py)."""
+    for layer in cache_list:
+        pages = layer.get("pages") if layer is not None else None
+        if pages is None:
+            continue
+        pool = pages.pool
+        pool.reserve_all(n_tokens)
+
+
 def _accounting(m):
     if hasattr(m, "decide_attention_path") and hasattr(m, "_record_attention_call"):
         return m.decide_attention_path, m._record_attention_call, getattr(m, "_ATTENTION_PHASE", "other")
@@ -126,6 +140,8 @@ def _fp8v_forward(self, x, cos, sin, cache=None):
     k = m.apply_rope(k, cos, sin)
 
     if cache is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise SdvError("a prefill from an empty cache creates the page pool; run it before recording a graph")
         pool = PagedKVCache(KV, D, batch=b, capacity_tokens=max(_OPTS["capacity_tokens"], s), device=x.device,
                             seed=_OPTS["seed"], scale_mode=_OPTS["scale_mode"])
         pages = LayerPages(pool)

@@ -99,7 +99,8 @@ def test_append_attention_host_validation(lib):
                                               a["D"], a["T"], a["tm"], a["ws"], a["wsb"], a["out"], a["kn"], a["vn"],
                                               a["slots"], a["nls"], a["mode"], a["st"])
     assert f(kn=N) == _native.SDV_ERR_NULL
-    assert f(slots=N) == _native.SDV_ERR_NULL
+    assert f(slots=N, D=96) == _native.SDV_ERR_UNSUPPORTED         # NULL slots (from the block table) are valid
+    assert f(sl=N, D=96) == _native.SDV_ERR_UNSUPPORTED            # NULL lengths (all max_seq_len) are valid
     assert f(q=N) == _native.SDV_ERR_NULL                         # the attention checks apply
     assert f(mode=5) == _native.SDV_ERR_UNSUPPORTED
     assert f(vn=ctypes.c_void_p(0x1008)) == _native.SDV_ERR_ALIGN

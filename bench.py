@@ -17,6 +17,7 @@ Prints ONE JSON line.  `value` is whole-step throughput in GB/s of algorithmic b
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -30,6 +31,36 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "specdec-context-scaling_amd"))
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_decode8k_multi.json"
+
+
+def kernel_source_sha256() -> str:
+    """Digest of the native sources (csrc/*, include/sdv.h): a traffic figure measured on other
+    sources is not this build's."""
+    h = hashlib.sha256()
+    files = sorted((ROOT / "specdec-context-scaling_amd" / "csrc").iterdir()) + [ROOT / "include" / "sdv.h"]
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+def stamped_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary, and where they came from; the bytes are None when that summary was measured on
+    other native sources than the ones built here."""
+    if not TRAFFIC_FILE.exists():
+        return None, {"file": None, "reason": "no traffic summary committed"}
+    rec = json.loads(TRAFFIC_FILE.read_text())
+    cur = kernel_source_sha256()
+    src = {"file": str(TRAFFIC_FILE.relative_to(ROOT)), "summary": rec.get("summary"),
+           "measured_source_sha256": rec.get("source_sha256"), "current_source_sha256": cur}
+    if rec.get("source_sha256") != cur:
+        src["reason"] = "measured on other native sources: stale, not reported"
+        return None, src
+    return rec.get("bytes_per_launch", {}).get(kernel), src
+
+
 L, B, H, KV, D, T, S = 28, 1, 12, 2, 128, 8192, 1
 
 
@@ -206,10 +237,7 @@ def main():
                      "frac_of_peak": round(bytes_step / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "launches_per_step": L * (1 if ops.single_launch_workgroups(1, B, H, KV, S, D, T) else 3)}
 
-    traffic = None
-    tf = ROOT / "profiles" / "traffic_decode8k_multi.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get(dom)
+    traffic, traffic_src = stamped_traffic(dom)
 
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -249,7 +277,8 @@ def main():
         "three_launch_us": {k: round(v, 3) for k, v in three.items()},
         "roofline": {"bound": "hbm", "kernel": f"{dom}_kernel (multi-layer call)", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3), "traffic": traffic},
+                     "bytes_per_launch": dom_bytes, "us_per_launch": round(dom_us, 3), "traffic": traffic,
+                     "traffic_source": traffic_src},
         "per_layer_graph": graph_leg,
         "cpu_baseline": cpu,
         "configs": configs,
@@ -361,6 +390,9 @@ def suite(torch, dev, reps8k, time_steps, cpu=True):
     del creps
     torch.cuda.empty_cache()
 
+    # row f2: the engine's draft chain and verify block through the pack, eager and from a graph
+    out["f2_engine_graph"] = engine_rows(torch, dev)
+
     # row f3: the reference's prefill chunk (2048 query rows over 8192 keys), target and draft
     out["f3_prefill_chunk_target_2048x8192"] = prefill_row(torch, dev, 12, 2, 128, 2048, 8192,
                                                            ref={"cudnn_sdpa_ms": 4.56, "cudnn_sdpa_transient_MiB": 74.1,
@@ -441,6 +473,184 @@ def prefill_row(torch, dev, h, kv, d, s, t, ref, nrep=2):
             "TFLOPs_algorithmic": round(flops / (us * 1e-6) / 1e12, 1),
             "TFLOPs_executed": round(executed / (us * 1e-6) / 1e12, 1),
             "reference_rtx4060": ref}
+
+
+# ---------------------------------------------------------------------------- engine host for the pack
+# The pack (specdec_amd.kernels.patch) replaces SelfAttention.forward of an engine module, as the
+# reference's kernels/patch.py does for specdec.engine.model_self.  The rows below need a
+# full-size host to record the engine's own steps: a Qwen2-shaped decoder (RMSNorm, rotate-half
+# RoPE, biased q/k/v projections, SiLU-gated MLP, tied LM head) with random weights, built here;
+# every attention call goes through the pack.
+def _qwen_module(torch):
+    import types
+
+    nn = torch.nn
+    F = torch.nn.functional
+    mod = types.ModuleType("bench_qwen")
+
+    class RMSNorm(nn.Module):
+        def __init__(self, n):
+            super().__init__()
+            self.weight = nn.Parameter(torch.ones(n))
+
+        def forward(self, x):
+            xf = x.float()
+            return self.weight * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype)
+
+    def rope(head_dim, n, start, device, dtype):
+        inv = 1.0 / (1e6 ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
+        ang = torch.outer(torch.arange(start, start + n, device=device, dtype=torch.float32), inv)
+        return torch.cat([ang.cos()] * 2, -1)[None, None].to(dtype), torch.cat([ang.sin()] * 2, -1)[None, None].to(dtype)
+
+    def apply_rope(x, cos, sin):
+        h = x.shape[-1] // 2
+        return x * cos + torch.cat([-x[..., h:], x[..., :h]], -1) * sin
+
+    class SelfAttention(nn.Module):
+        def __init__(self, hidden, heads, kv, hd):
+            super().__init__()
+            self.q_proj = nn.Linear(hidden, heads * hd)
+            self.k_proj = nn.Linear(hidden, kv * hd)
+            self.v_proj = nn.Linear(hidden, kv * hd)
+            self.o_proj = nn.Linear(heads * hd, hidden, bias=False)
+            self.heads, self.kv_heads, self.head_dim, self.kv_format = heads, kv, hd, "v_fp8"
+
+        def forward(self, x, cos, sin, cache=None):
+            raise RuntimeError("install the fp8v pack")
+
+    class Layer(nn.Module):
+        def __init__(self, hidden, heads, kv, hd, inter):
+            super().__init__()
+            self.self_attn = SelfAttention(hidden, heads, kv, hd)
+            self.input_layernorm, self.post_attention_layernorm = RMSNorm(hidden), RMSNorm(hidden)
+            self.gate_proj = nn.Linear(hidden, inter, bias=False)
+            self.up_proj = nn.Linear(hidden, inter, bias=False)
+            self.down_proj = nn.Linear(inter, hidden, bias=False)
+
+        def forward(self, x, cos, sin, cache):
+            a, c = self.self_attn(self.input_layernorm(x), cos, sin, cache)
+            x = x + a
+            y = self.post_attention_layernorm(x)
+            return x + self.down_proj(F.silu(self.gate_proj(y)) * self.up_proj(y)), c
+
+    class Model(nn.Module):
+        def __init__(self, vocab, hidden, heads, kv, hd, inter, layers):
+            super().__init__()
+            self.embed = nn.Embedding(vocab, hidden)
+            self.layers = nn.ModuleList(Layer(hidden, heads, kv, hd, inter) for _ in range(layers))
+            self.norm = RMSNorm(hidden)
+            self.head_dim = hd
+
+        def run(self, ids, cache):
+            """Logits of ids (1, s) given the per-layer cache list (None: prefill)."""
+            x = self.embed(ids)
+            start = 0 if cache is None else cache[0]["k"].shape[2]
+            cos, sin = rope(self.head_dim, ids.shape[1], start, x.device, x.dtype)
+            new = []
+            for i, layer in enumerate(self.layers):
+                x, c = layer(x, cos, sin, None if cache is None else cache[i])
+                new.append(c)
+            return self.norm(x) @ self.embed.weight.T, new
+
+    mod.SelfAttention, mod.apply_rope, mod.Model = SelfAttention, apply_rope, Model
+    return mod
+
+
+def engine_rows(torch, dev):
+    """The engine's own speculative steps through the pack, eager and replayed from a HIP graph, at
+    8K context: the draft chain (5 proposal steps of the 0.5B shape: hidden 896, 14/2/64, 24
+    layers, vocab 151936) and the target verify block (5 rows of the 1.5B shape: hidden 1536,
+    12/2/128, 28 layers), beside the reference's graph experiments (README.md:113-115:
+    draft-chain speed-up 3.7-6.0x and verify 1.4-2.6x on its RTX 4060 Laptop, graph pools 2.0 /
+    0.89 GiB).  Weights are random (no checkpoints offline); the contexts are prefilled through
+    the pack in 2048-token chunks (the prefill kernels), then recorded at that fixed length."""
+    from specdec_amd.kernels import patch
+
+    mod = _qwen_module(torch)
+    out = {}
+    shapes = {"draft_chain_0p5B_5x24_T8192": (896, 14, 2, 64, 4864, 24, "propose"),
+              "target_verify_1p5B_5rows_28L_T8192": (1536, 12, 2, 128, 8960, 28, "verify")}
+    g = torch.Generator(device=dev)
+    g.manual_seed(951)
+    patch.install("fp8v", mod, scale_mode="rcp", capacity_tokens=8192 + 64, seed=17)
+    try:
+        for name, (hidden, heads, kv, hd, inter, layers, phase) in shapes.items():
+            _progress(f"engine {name}")
+            with torch.device(dev):
+                model = mod.Model(151936, hidden, heads, kv, hd, inter, layers).to(torch.bfloat16).eval()
+            with torch.no_grad():
+                for prm in model.parameters():
+                    if prm.dim() == 2:
+                        prm.normal_(0.0, 1.0 / prm.shape[1] ** 0.5, generator=g)
+                model.embed.weight.mul_(0.05)
+            ids = torch.randint(0, 151936, (1, 8192), generator=g, device=dev)
+            toks = torch.randint(0, 151936, (1, 5), generator=g, device=dev)
+            with torch.no_grad():
+                cache = None
+                for c0 in range(0, 8192, 2048):
+                    _, cache = model.run(ids[:, c0:c0 + 2048], cache)
+                patch.reserve(cache, 8192 + 5)
+
+            def step():
+                view = [dict(layer) for layer in cache]
+                with torch.no_grad():
+                    if phase == "verify":
+                        return model.run(toks, view)[0]
+                    lg = None
+                    for i in range(5):
+                        lg, view = model.run(toks[:, i:i + 1], view)
+                    return lg
+
+            for _ in range(3):
+                step()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            e0.record()
+            for _ in range(reps):
+                step()
+            e1.record()
+            torch.cuda.synchronize()
+            eager_us = e0.elapsed_time(e1) * 1e3 / reps
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                step()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            # the graph's memory: the peak of what the recorded step allocated (activations and
+            # logits; the cache is written in place, so nothing of it lands in the graph's pool).
+            # Recording on the warmed-up side stream keeps the BLAS library's per-stream
+            # workspace, made on that stream's first GEMM, out of the figure.
+            alloc0 = torch.cuda.memory_allocated(dev)
+            torch.cuda.reset_peak_memory_stats(dev)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                logits = step()
+            torch.cuda.synchronize()
+            pool_peak = torch.cuda.max_memory_allocated(dev) - alloc0
+            pool_kept = torch.cuda.memory_allocated(dev) - alloc0
+            graph.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            graph_us = e0.elapsed_time(e1) * 1e3 / reps
+            out[name] = {"eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
+                         "speedup": round(eager_us / graph_us, 2),
+                         "graph_pool_peak_MiB": round(pool_peak / 2 ** 20, 1),
+                         "graph_outputs_MiB": round(pool_kept / 2 ** 20, 1),
+                         "logits_shape": list(logits.shape),
+                         "attention_calls": layers * (5 if phase == "propose" else 1),
+                         "reference_rtx4060": {"graph_pool_GiB": 2.0 if phase == "propose" else 0.89,
+                                               "speedup": "3.7-6.0x" if phase == "propose" else "1.4-2.6x"}}
+            del graph, model, cache, logits
+            torch.cuda.empty_cache()
+    finally:
+        patch.restore()
+    return out
 
 
 def chain_row(torch, dev, reps, layers, h, kv, d, T, s, steps, fused=False):

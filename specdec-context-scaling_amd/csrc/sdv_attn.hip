@@ -669,6 +669,27 @@ static_assert(kSyncBytes == SDV_SYNC_BYTES, "sdv.h states the synchronisation pr
 constexpr uint32_t kTagGraph = 0x80000000u;  // tag bit of a graph-recorded call
 constexpr uint32_t kDefaultSpinLimit = 1u << 20;
 
+// Phase timeline of the single launch, in builds with SDV_PHASE_TRACE only (libsdv_trace.so):
+// thread 0 of each of the first kPhaseTraceGroups workgroups stamps the 100 MHz wall clock at
+// the phase boundaries 0..9 (start, table + append done, q.k^T done, statistics published,
+// group statistics read, p.V done, partial published, owner polls done, output written, end)
+// into its kPhaseSlots words; sdv_phase_trace_read copies the array to the host.  The product
+// library compiles the stamps away.
+constexpr int kPhaseSlots = 16;
+constexpr int kPhaseTraceGroups = 4096;
+#ifdef SDV_PHASE_TRACE
+__device__ unsigned long long phase_trace[kPhaseTraceGroups * kPhaseSlots];
+#define SDV_PHASE(k)                                                                        \
+  do {                                                                                      \
+    if (threadIdx.x == 0 && blockIdx.x < kPhaseTraceGroups)                                 \
+      phase_trace[blockIdx.x * kPhaseSlots + (k)] = wall_clock64();                         \
+  } while (0)
+#else
+#define SDV_PHASE(k) \
+  do {               \
+  } while (0)
+#endif
+
 __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
   return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)tag << 32);
 }
@@ -774,6 +795,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   __shared__ int s_next, s_next2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int item = blockIdx.x;
+  SDV_PHASE(0);
   const int big = a.f_extra * (a.f_base + 1);  // workgroups of the groups with one more item
   int grp, c, n_g, item0;
   if (item < big) {
@@ -852,6 +874,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   }
   __syncthreads();
 
+  SDV_PHASE(1);
   // ------------------------------------------------------------------ 1. q.k^T
   bf16x8 qop[NT][KK];
   int qsi[NT];
@@ -956,6 +979,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   SDV_VMCNT0();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  SDV_PHASE(2);
   uint64_t* fs = sync_stats(a);
   // the item's statistics of each row, merged in an order that does not depend on which
   // wavefront took which block in q.k^T.  One row per wavefront (decode): lane l merges
@@ -1009,6 +1033,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     if (act && sl == 0) publish_stat(row, m, l);
   }
 
+  SDV_PHASE(3);
   // ------------------------------------------------------------------ 2. p.V
   const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
   const float* slayer = a.v_scales + layer * a.s_ls;
@@ -1216,6 +1241,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     int u0 = claim2();
     load_u(u0, ua);
     group_stats(gm, ginv);
+    SDV_PHASE(4);
     // p formed once per (row, token) before the loop: a unit covers half the dimensions of
     // its blocks, so forming p per unit would repeat every exp (28 layers at 8K: 39.2 ->
     // 37.2 us together with the single-exit loops)
@@ -1232,6 +1258,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       more = u0 < nunits;
     }
     __syncthreads();
+    SDV_PHASE(5);
     // the item's partial: unit slots summed in stage order
     for (int o4 = tid; o4 * 4 < a.R * D; o4 += NTHR) {
       f32x4 v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
@@ -1275,6 +1302,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
     }
     group_stats(gm, ginv);
+    SDV_PHASE(4);
     if (poll_first && wave < NT) {
   #pragma unroll
       for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
@@ -1371,6 +1399,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     // every wavefront is past its statistics before any partial is published (an owner that
     // has seen all partials clears the statistics)
     __syncthreads();
+    SDV_PHASE(5);
     if (pt == 0) {
   #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
@@ -1389,6 +1418,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     }
   }
 
+  SDV_PHASE(6);
   // ------------------------------------------------------------------ 3. output
   // Workgroup c < nvq of the group owns output chunks [lo, lo + w) (16 bytes each) and sums
   // them over the group's items in item order.  Partial words are never 0 once written, and
@@ -1464,6 +1494,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   else
     poll_chunks_many();
   __syncthreads();
+  SDV_PHASE(7);
   // a wait of this workgroup expired: its outputs become NaN, the error is counted (and a
   // graph-recorded call poisons the workspace), and nothing is cleared
   if (s_fail) {
@@ -1530,6 +1561,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     uint16_t* dst = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d;
     *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(sm.x, sm.y), pack_bf16x2(sm.z, sm.w));
   }
+  SDV_PHASE(8);
   if (c < nown) {
     for (int e = c + tid * nown; e < nvq * a.R; e += NTHR * nown) {
       uint64_t* p = fs + 2 * ((int64_t)(item0 + e / a.R) * 64 + e % a.R);
@@ -1537,6 +1569,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       store_dev_u64(p + 1, 0);
     }
   }
+  SDV_PHASE(9);
 }
 
 
@@ -2322,6 +2355,18 @@ extern "C" int sdv_attention_set_wait_limit(uint32_t polls) {
   g_wait_limit.store(polls, std::memory_order_relaxed);
   return SDV_OK;
 }
+
+#ifdef SDV_PHASE_TRACE
+// Trace builds only: copies the phase stamps of the last single launch (workgroup i's stamps at
+// words [16 i, 16 i + 10)) to host memory; synchronous on the current device.
+extern "C" int sdv_phase_trace_read(unsigned long long* dst, size_t words) {
+  if (!dst) return SDV_ERR_NULL;
+  if (words > (size_t)kPhaseTraceGroups * kPhaseSlots) return SDV_ERR_SHAPE;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(phase_trace), words * 8, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? SDV_OK
+             : SDV_ERR_HIP;
+}
+#endif
 
 extern "C" int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,
                                               int32_t q_len, int32_t head_dim, int32_t max_seq_len) {

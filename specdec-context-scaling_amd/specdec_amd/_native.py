@@ -82,8 +82,11 @@ class SdvError(RuntimeError):
 _LIB = None
 
 
-def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
-    """Load libsdv.so once and attach the C signatures.  Raises SdvError when it is absent."""
+def load(path: os.PathLike | str | None = None, make_default: bool = False) -> ctypes.CDLL:
+    """Load libsdv.so once and attach the C signatures.  Raises SdvError when it is absent.
+
+    path: another build of the same sources (the phase-trace variant); make_default=True makes
+    it the library every op of this process calls from then on."""
     global _LIB
     if _LIB is not None and path is None:
         return _LIB
@@ -98,7 +101,7 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         fn.argtypes = args
     if lib.sdv_abi_version() != ABI_VERSION:
         raise SdvError(f"{p} has ABI {lib.sdv_abi_version()}, expected {ABI_VERSION}; rebuild it")
-    if path is None:
+    if path is None or make_default:
         _LIB = lib
     return lib
 

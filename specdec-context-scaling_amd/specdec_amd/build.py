@@ -6,6 +6,7 @@ Here the native code is a plain C-ABI shared library compiled ahead of time, in-
 ``load()`` keeps the reference's name and its "build once, cache the module" behaviour.
 
     python -m specdec_amd.build          # compile specdec_amd/libsdv.so
+    python -m specdec_amd.build --trace  # compile specdec_amd/libsdv_trace.so (phase stamps)
 """
 from __future__ import annotations
 
@@ -45,11 +46,19 @@ def _hipcc() -> str:
     raise _native.SdvError("hipcc not found (ROCm is required to build libsdv.so)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into specdec_amd/libsdv.so (always recompiles)."""
-    out = _native.LIB_PATH
+TRACE_LIB_PATH = PKG_DIR / "libsdv_trace.so"
+
+
+def build(verbose: bool = False, trace: bool = False) -> Path:
+    """Compile every HIP source into specdec_amd/libsdv.so (always recompiles).
+
+    trace=True builds the phase-trace variant, specdec_amd/libsdv_trace.so: the same kernels
+    with wall-clock stamps at the single launch's phase boundaries (SDV_PHASE_TRACE), read by
+    specdec_amd.phase_trace.  The product path never loads it."""
+    out = TRACE_LIB_PATH if trace else _native.LIB_PATH
     tmp = out.with_suffix(".so.tmp")
-    cmd = [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(tmp), *map(str, sources())]
+    defs = ["-DSDV_PHASE_TRACE"] if trace else []
+    cmd = [_hipcc(), *HIPCC_FLAGS, *defs, f"-I{INCLUDE}", f"-I{CSRC}", "-o", str(tmp), *map(str, sources())]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     msgs = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
@@ -67,4 +76,4 @@ def load():
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, trace="--trace" in sys.argv))

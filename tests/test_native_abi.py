@@ -154,3 +154,19 @@ def test_encode_validation(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_native.SdvError, match="not built"):
         _native.load(tmp_path / "libsdv.so")
+
+
+def test_phase_trace_stays_out_of_the_product_library(lib):
+    """The phase stamps (SDV_PHASE_TRACE) exist only in libsdv_trace.so, which exports the same
+    C-ABI plus its reader; the product library compiles them away."""
+    assert not hasattr(lib, "sdv_phase_trace_read")
+    if not build.TRACE_LIB_PATH.exists():
+        pytest.skip("libsdv_trace.so not built")
+    tlib = ctypes.CDLL(str(build.TRACE_LIB_PATH))
+    for n in _declared():
+        assert hasattr(tlib, n), n
+    tlib.sdv_phase_trace_read.restype = ctypes.c_int
+    tlib.sdv_phase_trace_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    assert tlib.sdv_phase_trace_read(None, 1) == _native.SDV_ERR_NULL
+    buf = (ctypes.c_uint64 * 1)()
+    assert tlib.sdv_phase_trace_read(buf, 1 << 40) == _native.SDV_ERR_SHAPE

@@ -34,29 +34,26 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_decode8k_multi.json"
 
 
-def kernel_source_sha256() -> str:
-    """Digest of the native sources (csrc/*, include/sdv.h): a traffic figure measured on other
-    sources is not this build's."""
-    h = hashlib.sha256()
-    files = sorted((ROOT / "specdec-context-scaling_amd" / "csrc").iterdir()) + [ROOT / "include" / "sdv.h"]
-    for f in files:
-        h.update(f.name.encode())
-        h.update(f.read_bytes())
-    return h.hexdigest()
+def library_sha256() -> str:
+    """Digest of the native library this run loads (libsdv.so; rebuilding the same sources gives
+    the same bytes): a traffic figure measured on another build is not this build's."""
+    from specdec_amd import _native
+
+    return hashlib.sha256(_native.LIB_PATH.read_bytes()).hexdigest()
 
 
 def stamped_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary, and where they came from; the bytes are None when that summary was measured on
-    other native sources than the ones built here."""
+    another build of the native library than the one this run loads."""
     if not TRAFFIC_FILE.exists():
         return None, {"file": None, "reason": "no traffic summary committed"}
     rec = json.loads(TRAFFIC_FILE.read_text())
-    cur = kernel_source_sha256()
+    cur = library_sha256()
     src = {"file": str(TRAFFIC_FILE.relative_to(ROOT)), "summary": rec.get("summary"),
-           "measured_source_sha256": rec.get("source_sha256"), "current_source_sha256": cur}
-    if rec.get("source_sha256") != cur:
-        src["reason"] = "measured on other native sources: stale, not reported"
+           "measured_library_sha256": rec.get("library_sha256"), "this_library_sha256": cur}
+    if rec.get("library_sha256") != cur:
+        src["reason"] = "measured on another build of libsdv.so: stale, not reported"
         return None, src
     return rec.get("bytes_per_launch", {}).get(kernel), src
 

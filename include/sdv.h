@@ -113,13 +113,15 @@ size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q
 /*
  * Zero the workspace's synchronisation area (its first SDV_SYNC_BYTES bytes) on `stream`.
  * Call it once after allocating a workspace and before its first sdv_paged_attention; every
- * call that completes normally leaves the area zero again.  No counterpart in the reference
- * (it has no workspace).
+ * call that completes normally leaves the statistics zero again (the partial slots keep the
+ * last call's values; each item zeroes its own slot at the start of the next call).  No
+ * counterpart in the reference (it has no workspace).
  *
- * The single-launch path exchanges (max, sum) statistics and fp32 partials between
- * workgroups through this area as 64-bit (value, call tag) words; a reader takes a word only
- * when it carries its own call's tag, so a word an earlier call left behind is never read
- * as current.  Its waits are bounded (they only expire when the grid's workgroups cannot all
+ * The single-launch path exchanges (max, sum) statistics between workgroups through this
+ * area as 64-bit (value, call tag) words; a reader takes a word only when it carries its own
+ * call's tag, so a word an earlier call left behind is never read as current.  fp32 partials
+ * travel as bits + 1 (0 = not yet written) in slots that their item zeroes, and waits for,
+ * before it publishes its statistics.  Its waits are bounded (they only expire when the grid's workgroups cannot all
  * be resident at once: another process holding CUs, a CU mask): an expired wait makes the
  * outputs it could not complete NaN and counts in word 0 of the area.  A call recorded into
  * a HIP graph (its replays reuse one tag) that expires also sets word 1; while it is set,

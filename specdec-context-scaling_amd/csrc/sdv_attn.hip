@@ -613,18 +613,17 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
 // scheduler favours takes more blocks and all finish together.  Per workgroup:
 //   1. q.k^T over the item's blocks: BF16 scores and per-block (max, sum) of every row into
 //      LDS; the item's (max, sum) -- merged over its blocks in block order, so it does not
-//      depend on which wavefront took which block -- published to device memory.  A
-//      published entry is never all-zero bits (sum >= 1, or max = -inf), so zero means "not
-//      yet": no counter is needed for this step.
-//   2. Once every non-empty item of the group has published (one wavefront polls, the
-//      others keep their first V loads in flight), the group's statistics are merged in a
+//      depend on which wavefront took which block -- published to device memory as words
+//      tagged with the call (below): no counter is needed for this step.
+//   2. Once every item of the group has published (one wavefront polls, the others keep
+//      their first V loads in flight), the group's statistics are merged in a
 //      fixed order; the item's scores in LDS become p = bf16(exp(s - M) / L) in place, once
 //      per (row, token); the wavefronts run p.V over the item's blocks; per-unit results
 //      are summed in LDS in order and the fp32 partial is published.
 //   3. Workgroup c of the group owns a slice of the outputs: it polls the slice of every
 //      item's partial, sums it over the items in order (the result does not depend on the
-//      order workgroups finish) into the BF16 output, and clears what it read plus a share of
-//      the statistics for the next call.
+//      order workgroups finish) into the BF16 output, and clears a share of the statistics
+//      for the next call (partial slots are zeroed by their own item at the next call's start).
 // Cross-workgroup data moves through device-scope (sc1) stores and loads, which bypass the
 // per-XCD L2 caches; no counter, ticket or cache-writeback fence is needed (on gfx950 each
 // agent-scope release costs ~40 ns and serialises chip-wide; a counter round trip costs ~1.3 us

@@ -15,8 +15,8 @@ replays, in microseconds).
 
 Workloads (the Qwen2.5-1.5B attention shape, 12 query / 2 KV heads of 128, T = 8192):
 one_layer_decode (an engine decode call), one_layer_verify (S=5), multi_layer_decode (all 28
-layers in one call, the headline); and the 0.5B draft's layer (14 / 2 heads of 64),
-draft_one_layer_decode.
+layers in one call, the headline), multi_layer_verify (S=5); and the 0.5B draft's shape (14 / 2
+heads of 64): draft_one_layer_decode, draft_multi_layer_decode (24 layers).
 """
 from __future__ import annotations
 
@@ -42,7 +42,9 @@ WORKLOADS = {
     "one_layer_decode": (1, 12, 2, 128, 1, 8192),
     "one_layer_verify": (1, 12, 2, 128, 5, 8192),
     "multi_layer_decode": (28, 12, 2, 128, 1, 8192),
+    "multi_layer_verify": (28, 12, 2, 128, 5, 8192),
     "draft_one_layer_decode": (1, 14, 2, 64, 1, 8192),
+    "draft_multi_layer_decode": (24, 14, 2, 64, 1, 8192),
 }
 
 

@@ -403,7 +403,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v, backend: str = "hip") -> torc
     if payload.shape != k.shape or tuple(scale.shape) != tuple(k.shape[:3]) + (1,):
         _fail(f"v payload {tuple(payload.shape)} / scale {tuple(scale.shape)} do not match k {tuple(k.shape)}")
     kp, vp, vs, bt, sl = pack_contiguous(k.contiguous(), payload.contiguous(), scale.contiguous())
-    return paged_attention(q.contiguous(), kp, vp, vs, bt, sl, k.shape[2])
+    return torch.ops.sdv.paged_attention(q.contiguous(), kp, vp, vs, bt, sl, k.shape[2])
 
 
 def fp8_encode(x: torch.Tensor) -> torch.Tensor:
@@ -412,3 +412,48 @@ def fp8_encode(x: torch.Tensor) -> torch.Tensor:
     out = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     _native.check(_native.load().sdv_fp8_encode(_p(x), _p(out), x.numel(), _stream(x.device)), "sdv_fp8_encode")
     return out
+
+
+# ---------------------------------------------------------------------------- torch.library
+# The ops as torch custom operators (namespace "sdv"), so torch.compile and fake-tensor tracing
+# see them: the real implementations are the functions above (the C ABI through ctypes); the
+# fake implementations only produce outputs of the right shape and dtype.  The page tensors of
+# the appending ops are declared mutated.
+@torch.library.custom_op("sdv::paged_attention", mutates_args=())
+def _lib_paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, v_scales: torch.Tensor,
+                         block_table: torch.Tensor, seq_lens: torch.Tensor | None, max_seq_len: int,
+                         q_token_major: bool = False) -> torch.Tensor:
+    return paged_attention(q, k_pages, v_pages, v_scales, block_table, seq_lens, max_seq_len,
+                           q_token_major=q_token_major)
+
+
+@_lib_paged_attention.register_fake
+def _(q, k_pages, v_pages, v_scales, block_table, seq_lens, max_seq_len, q_token_major=False):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("sdv::paged_attention_append", mutates_args=("k_pages", "v_pages", "v_scales"))
+def _lib_paged_attention_append(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                                v_scales: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor | None,
+                                max_seq_len: int, k_new: torch.Tensor, v_new: torch.Tensor,
+                                slot_mapping: torch.Tensor | None, scale_mode: str = "div",
+                                q_token_major: bool = False) -> torch.Tensor:
+    return paged_attention(q, k_pages, v_pages, v_scales, block_table, seq_lens, max_seq_len,
+                           q_token_major=q_token_major, append=(k_new, v_new, slot_mapping), scale_mode=scale_mode)
+
+
+@_lib_paged_attention_append.register_fake
+def _(q, k_pages, v_pages, v_scales, block_table, seq_lens, max_seq_len, k_new, v_new, slot_mapping,
+      scale_mode="div", q_token_major=False):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("sdv::quant_append", mutates_args=("k_pages", "v_pages", "v_scales"))
+def _lib_quant_append(v_new: torch.Tensor, slot_mapping: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                      v_scales: torch.Tensor, k_new: torch.Tensor | None = None, scale_mode: str = "div") -> None:
+    quant_append(v_new, slot_mapping, k_pages, v_pages, v_scales, k_new, scale_mode=scale_mode)
+
+
+@_lib_quant_append.register_fake
+def _(v_new, slot_mapping, k_pages, v_pages, v_scales, k_new=None, scale_mode="div"):
+    return None

@@ -28,6 +28,7 @@
 // MFMA 16x16x32 lane layout (measured on gfx950): A lane l supplies row l%16, B lane l
 // supplies column l%16, both with the same 8 k-slots for lane group l/16; the result lane
 // l holds rows 4*(l/16)+i, column l%16.  Every operand below uses that mapping.
+#include <algorithm>
 #include <atomic>
 #include <climits>
 #include <mutex>
@@ -683,10 +684,22 @@ __device__ unsigned long long phase_trace[kPhaseTraceGroups * kPhaseSlots];
     if (threadIdx.x == 0 && blockIdx.x < kPhaseTraceGroups)                                 \
       phase_trace[blockIdx.x * kPhaseSlots + (k)] = wall_clock64();                         \
   } while (0)
+// group_kernel accumulates per workgroup: words 10-12 = wall-clock ticks in claim + setup, q.k^T
+// (with the statistics merge) and p.V (with the output); word 13 = groups done.
+#define SDV_PHASE_ADD(k, v)                                                                 \
+  do {                                                                                      \
+    if (threadIdx.x == 0 && blockIdx.x < kPhaseTraceGroups)                                 \
+      phase_trace[blockIdx.x * kPhaseSlots + (k)] += (v);                                   \
+  } while (0)
+#define SDV_CLOCK() wall_clock64()
 #else
 #define SDV_PHASE(k) \
   do {               \
   } while (0)
+#define SDV_PHASE_ADD(k, v) \
+  do {                      \
+  } while (0)
+#define SDV_CLOCK() 0ull
 #endif
 
 __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
@@ -1832,6 +1845,247 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   }
 }
 
+// ---------------------------------------------------------------------------- group
+// Many (layer*batch, KV head) groups of one row tile each -- decode and short verify over many
+// sequences (config 4: 28 layers x 32 ragged sequences x 2 KV heads = 1792 groups) -- in one
+// launch of persistent workgroups, one per CU, that take whole groups from a claim counter in
+// the order of decreasing sequence length (the long groups first, the short ones last, so the
+// workgroups finish together).  A group is done by one workgroup alone and no workgroup ever
+// waits for another:
+//   1. q.k^T: wavefront w takes blocks w, w+W, ... (two in flight); the BF16 scores of row n go
+//      to the workgroup's own scratch rows in the workspace, and
+//      each wavefront keeps a running (max, sum) per row, rescaled exactly (factor 1 while the
+//      max stays).
+//   2. The wavefronts' pairs are merged in wavefront order in LDS: (M, 1/L) per row.
+//   3. p.V: wavefront w takes stages of 4 blocks w, w+W, ... (lane group g: block 4*stage + g),
+//      p = bf16(exp(s - M) / L) from the scratch scores, V dequantized in registers, O^T on the
+//      MFMA (pv_compute, as in the three-launch p.V kernel); the wavefronts' outputs are summed in
+//      wavefront order in LDS and stored as BF16.
+// Every reduction has a fixed order, so results do not depend on which workgroup took which
+// group.  Words 2 and 3 of the synchronisation area hold the claim counter and the count of
+// finished workgroups; the last workgroup to finish zeroes both for the next call.
+constexpr int kGroupWaves = 8;
+constexpr int kGroupGrid = 256;          // workgroups (one per CU of the MI355X)
+constexpr int kGroupMaxBlocks = 4096;    // page ids of one group staged in LDS: T <= 65536
+constexpr int kGroupSortMax = 1024;      // batches up to this size are ordered by length
+constexpr int kGroupMinGroups = 1024;    // fewer groups: the three-launch path spreads them wider
+// K blocks and V stages (4 blocks) in flight per wavefront.  Deeper rings measured no faster on
+// config 4 (K 3-4, V 3: 2.55-2.60 ms against 2.54 ms)
+constexpr int kGroupKRing = 2;
+constexpr int kGroupVRing = 2;
+static_assert(kGroupSortMax <= kGroupMaxBlocks, "the lengths are staged in the page-id array");
+
+template <int D>
+__global__ __launch_bounds__(64 * kGroupWaves) void group_kernel(AttnArgs a, int n_groups, int layers, int tpad) {
+  constexpr int W = kGroupWaves, NTHR = 64 * W, KK = D / 32, DT = D / 16;
+  __shared__ int s_order[kGroupSortMax];
+  __shared__ int lpb[kGroupMaxBlocks];
+  __shared__ float2 lst[W][16];
+  __shared__ float2 lgs[16];
+  __shared__ float lacc[W][16][D + 4];  // +4: spread the lane groups over LDS banks
+  __shared__ int s_claim;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int per_seq = layers * a.KV;
+  const bool sorted = a.B <= kGroupSortMax;
+  if (sorted) {  // s_order[rank] = sequence: decreasing length, lower index first on ties
+    int* s_len = lpb;  // the lengths, staged in the page-id array before its first use
+    for (int b = tid; b < a.B; b += NTHR) s_len[b] = seq_len_of(a, b);
+    __syncthreads();
+    for (int b = tid; b < a.B; b += NTHR) {
+      const int tb = s_len[b];
+      int rank = 0;
+      for (int c = 0; c < a.B; ++c) {
+        const int tc = s_len[c];
+        rank += (tc > tb) || (tc == tb && c < b);
+      }
+      s_order[rank] = b;
+    }
+  }
+  uint16_t* scr = a.scores + (int64_t)blockIdx.x * a.R * tpad;  // this workgroup's score rows
+  const int prow = n < a.R ? n : 0;  // row this lane's probabilities come from (padding: row 0)
+#ifdef SDV_PHASE_TRACE
+  if (tid == 0 && blockIdx.x < kPhaseTraceGroups)
+    for (int w = 10; w < 14; ++w) phase_trace[blockIdx.x * kPhaseSlots + w] = 0;
+#endif
+  unsigned long long t0 = SDV_CLOCK();
+  for (;;) {
+    __syncthreads();  // the previous group's LDS reads are done (and s_order is written)
+    if (tid == 0) s_claim = (int)atomicAdd(a.sync + 2, 1u);
+    __syncthreads();
+    const int k = s_claim;
+    if (k >= n_groups) break;
+    const int rk = k / per_seq, rem = k - rk * per_seq;
+    const int layer = rem / a.KV, kvh = rem - layer * a.KV;
+    const int b = sorted ? s_order[rk] : rk;
+    const int T = seq_len_of(a, b);
+    const int nblk = (T + kBlock - 1) >> 4;
+
+    // q rows: lane (g, n) holds row n, dimensions kk*32 + 8g .. +7 (the B operand of S^T = K Q^T)
+    bf16x8 qop[KK];
+    int lim;  // last key row n sees
+    {
+      const bool rv = n < a.R;
+      const int hl = rv ? n / a.S : 0, si = rv ? n % a.S : 0;
+      const uint16_t* qp = a.q + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + g * 8;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) qop[kk] = rv ? load_bf16x8(qp + kk * 32) : zero_bf16x8();
+      lim = T - a.S + si;
+    }
+    const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
+    for (int j = tid; j < nblk; j += NTHR) {
+      const int pb = btrow[j];
+      lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
+    }
+    __syncthreads();
+    unsigned long long t1 = SDV_CLOCK();
+    SDV_PHASE_ADD(10, t1 - t0);
+
+    // ------------------------------------------------------------------ 1. q.k^T
+    float m_run = -INFINITY, l_run = 0.0f;  // row n; identical in the four lane groups
+    {
+      const uint16_t* kbase = a.k_pages + layer * a.k_ls + (int64_t)lane * 8;
+      // a block past the group reads block 0 (the wait counters stay exact) and is not computed
+      auto kload = [&](int j, bf16x8 (&kop)[KK], int& pb) {
+        pb = j < nblk ? lpb[j] : -1;
+        const uint16_t* kp = kbase + ((int64_t)max(pb, 0) * a.KV + kvh) * (kBlock * D);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) kop[kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + kk * 512));
+      };
+      auto kcompute = [&](const bf16x8 (&kop)[KK], int pb, int j) {
+        f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kk], qop[kk], acc, 0, 0, 0);
+        const int tb = j * kBlock + 4 * g;  // this lane's first token
+        float s4[4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = round_bf16(round_bf16(acc[i]) * a.inv_sqrt_d);
+          s4[i] = (pb >= 0 && tb + i <= lim) ? x : -INFINITY;
+          mt = fmaxf(mt, s4[i]);
+        }
+        if (n < a.R)
+          *reinterpret_cast<uint2*>(scr + (int64_t)n * tpad + tb) =
+              make_uint2(pack_bf16x2(s4[0], s4[1]), pack_bf16x2(s4[2], s4[3]));
+        // the block's (max, sum) of row n over the four lane groups, then the running pair
+        float2 pm = lane_pair<16>(mt);
+        float M = fmaxf(pm.x, pm.y);
+        pm = lane_pair<32>(M);
+        M = fmaxf(pm.x, pm.y);
+        const float nml = M == -INFINITY ? 0.0f : -M * kLog2e;  // empty block: every exp is 0
+        float l = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) l += __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml));
+        float2 pl = lane_pair<16>(l);
+        l = pl.x + pl.y;
+        pl = lane_pair<32>(l);
+        l = pl.x + pl.y;
+        const float mn = fmaxf(m_run, M);
+        const float f_old = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - mn) * kLog2e);
+        const float f_new = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((M - mn) * kLog2e);
+        l_run = l_run * f_old + l * f_new;
+        m_run = mn;
+      };
+      // a ring of kGroupKRing blocks in flight; one loop exit, at the head, and every buffer
+      // reloaded (kGroupKRing * W blocks ahead) right after it is used
+      bf16x8 kr[kGroupKRing][KK];
+      int pr[kGroupKRing];
+#pragma unroll
+      for (int i = 0; i < kGroupKRing; ++i) kload(wave + i * W, kr[i], pr[i]);
+      for (int j = wave; j < nblk; j += kGroupKRing * W) {
+#pragma unroll
+        for (int i = 0; i < kGroupKRing; ++i) {
+          const int jj = j + i * W;
+          if (jj < nblk) kcompute(kr[i], pr[i], jj);  // wave-uniform
+          kload(jj + kGroupKRing * W, kr[i], pr[i]);
+        }
+      }
+    }
+    if (g == 0) lst[wave][n] = make_float2(m_run, l_run);
+    __syncthreads();  // also makes the scratch scores visible to the whole workgroup
+
+    // ------------------------------------------------------------------ 2. (M, 1/L) per row
+    if (tid < 16) {
+      float m = lst[0][tid].x, l = lst[0][tid].y;
+#pragma unroll
+      for (int w = 1; w < W; ++w) merge_fast(m, l, lst[w][tid].x, lst[w][tid].y);
+      lgs[tid] = make_float2(m, 1.0f / l);
+    }
+    __syncthreads();
+    t0 = SDV_CLOCK();
+    SDV_PHASE_ADD(11, t0 - t1);
+
+    // ------------------------------------------------------------------ 3. p.V
+    float gm[1], ginv[1];
+    gm[0] = lgs[prow].x;
+    ginv[0] = lgs[prow].y;
+    f32x4 acc[DT][1];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt][0] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    {
+      const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
+      const float* slayer = a.v_scales + layer * a.s_ls;
+      const uint16_t* srow_p = scr + (int64_t)prow * tpad;
+      const int nst = (nblk + 3) >> 2;
+      const int full_blocks = T >> 4;
+      // lane group g takes block 4*st + g; a block past the group reads block 0 and the first
+      // block's scores, and is sanitized (no token) when its stage is computed
+      auto vload = [&](int st_i, PvStage<D, 1>& x) {
+        const int jb = 4 * st_i + g;
+        const int pb = jb < nblk ? lpb[jb] : -1;
+        x.ok = pb >= 0;
+        x.blk = jb;
+        const int64_t page = (int64_t)(x.ok ? pb : 0) * a.KV + kvh;
+        const uint8_t* vp = vlayer + (page * D + n) * kBlock;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) x.code[dt] = load_stream16(vp + dt * 16 * kBlock);
+        x.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
+        const uint4* ps = reinterpret_cast<const uint4*>(srow_p + (int64_t)(jb < nblk ? jb : 0) * kBlock);
+        x.sc[0][0] = ps[0];
+        x.sc[0][1] = ps[1];
+      };
+      PvStage<D, 1> vr[kGroupVRing];
+#pragma unroll
+      for (int i = 0; i < kGroupVRing; ++i) vload(wave + i * W, vr[i]);
+      for (int st_i = wave; st_i < nst; st_i += kGroupVRing * W) {
+#pragma unroll
+        for (int i = 0; i < kGroupVRing; ++i) {
+          const int ss = st_i + i * W;
+          if (ss < nst) pv_compute<D, 1>(vr[i], acc, gm, ginv, T, 4 * ss + 3 < full_blocks, n);  // wave-uniform
+          vload(ss + kGroupVRing * W, vr[i]);
+        }
+      }
+    }
+    // lane (g, n) holds O^T[dims dt*16 + 4g .. +3][row n]; the wavefronts are summed in order
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lacc[wave][n][dt * 16 + 4 * g + i] = acc[dt][0][i];
+    __syncthreads();
+    for (int e = tid; e * 4 < a.R * D; e += NTHR) {
+      const int r = (4 * e) / D, d = 4 * e - r * D;
+      float4 sm = *reinterpret_cast<const float4*>(&lacc[0][r][d]);
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        const float4 f = *reinterpret_cast<const float4*>(&lacc[w][r][d]);
+        sm.x += f.x; sm.y += f.y; sm.z += f.z; sm.w += f.w;
+      }
+      const int hl = r / a.S, si = r % a.S;
+      uint16_t* dst = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + d;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(sm.x, sm.y), pack_bf16x2(sm.z, sm.w));
+    }
+    t1 = SDV_CLOCK();
+    SDV_PHASE_ADD(12, t1 - t0);
+    SDV_PHASE_ADD(13, 1ull);
+    t0 = t1;
+  }
+  // the last workgroup to finish leaves the counters zero for the next call
+  if (tid == 0 && atomicAdd(a.sync + 3, 1u) == gridDim.x - 1) {
+    __hip_atomic_store(a.sync + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.sync + 3, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ---------------------------------------------------------------------------- planning
 struct Plan {
   int NT, n_row_groups, rpad;
@@ -1840,7 +2094,9 @@ struct Plan {
   int score_stride;
   size_t off_scores, off_stats, off_partial;     // three-launch layout (after the sync area)
   int64_t groups;
-  size_t total;                                   // bytes for either layout
+  bool group;                                     // group_kernel serves the call (many one-tile groups)
+  int tpad;                                       // group_kernel: scratch row length (tokens)
+  size_t total;                                   // bytes for every layout the call may take
 };
 
 static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len, Plan* p) {
@@ -1877,13 +2133,15 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->score_stride = max(p->n_qk_chunks * p->qk_chunk_tokens, p->n_pv_chunks * p->pv_chunk_tokens);
   const int64_t groups = (int64_t)L * B * KV;
   p->groups = groups;
+  p->group = false;
+  p->tpad = 0;
   if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) only
     p->off_scores = p->off_partial = kSyncBytes;
     p->off_stats = kSyncBytes;
     p->total = kSyncBytes + round_up((size_t)(groups * R * 8), 256);
     return true;
   }
-  // the sync area [0, kSyncBytes) is shared by both layouts and only the fused kernel uses it
+  // the sync area [0, kSyncBytes) is shared by every layout and only the fused kernel uses it
   const size_t scores = round_up((size_t)(groups * R * p->score_stride * 2), 256);
   const size_t stats = round_up((size_t)(groups * p->n_qk_chunks * p->rpad * 8), 256);
   const size_t partial = round_up((size_t)(groups * p->n_pv_chunks * R * D * 4), 256);
@@ -1892,6 +2150,12 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->off_partial = p->off_stats + stats;
   // the fused kernel keeps its statistics and partials inside the sync area
   p->total = p->off_partial + partial;
+  // group_kernel (words 2-3 of the sync area, then R scratch rows per workgroup at
+  // off_scores); the three-launch layout stays valid for the profiling entry point
+  p->group = p->NT == 1 && groups >= kGroupMinGroups && max_seq_len <= kGroupMaxBlocks * kBlock;
+  p->tpad = p->group ? (int)round_up((size_t)max_seq_len, kBlock) : 0;
+  if (p->group)
+    p->total = std::max(p->total, kSyncBytes + round_up((size_t)kGroupGrid * R * p->tpad * 2, 256));
   return true;
 }
 
@@ -2036,6 +2300,11 @@ static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t s
       default: done = try_fused<D, 4>(a, p, st); break;
     }
     if (done) return;
+    if (p.group) {  // many one-tile groups: persistent workgroups, whole groups each
+      hipLaunchKernelGGL(group_kernel<D>, dim3(kGroupGrid), dim3(64 * kGroupWaves), 0, st, a, (int)p.groups,
+                         zdim / a.B, p.tpad);
+      return;
+    }
   }
   switch (p.NT) {
     case 1: launch_qk_pv<D, 1>(a, p, zdim, st, phases); break;

@@ -1593,32 +1593,45 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // Shapes with more query rows than one row-tile group holds (R = G*S > 64: prefill and
 // chunked-prefill blocks, model_self.py:471-504, 637-648) in two launches whose workspace holds
 // only the per-row (max, sum) -- 8 bytes per row -- instead of the O(S*T) scores:
-//   pass 1  each wavefront takes 32 rows (two MFMA row tiles) and streams the page blocks its
+//   pass 1  each wavefront takes 16 rows (one MFMA row tile) and streams the page blocks its
 //           rows can see: S^T = K Q^T on MFMA (the K page is the A operand, the rows the B
 //           operand), scores rounded to BF16 twice, offset-causal mask, online (max, sum) per
 //           lane, merged over the lane groups into (M, L) per row.
-//   pass 2  the same wavefront streams the blocks again, two at a time, recomputes the BF16
-//           scores and forms p = bf16(exp(s - M) / L) in registers.  A lane's S^T fragment
-//           (row n, tokens 4g..4g+3 of each of the two blocks) is exactly the B operand of
-//           O^T = V_hat^T P^T with those 8 tokens as its k-slots, so the A operand is the
-//           matching 4-byte words of the dimension-major V pages (one wave load covers 16
-//           dimensions x 16 tokens of a page, contiguous), dequantized in registers
-//           (bf16(fp32(code) * scale)); O^T accumulates in fp32 and leaves as BF16, four
-//           dimensions of one row per lane.
+//   pass 2  the workgroup streams the blocks of its rows again, two at a time; each wavefront
+//           recomputes its rows' BF16 scores and forms p = bf16(exp(s - M) / L) in registers.
+//           A lane's S^T fragment (row n, tokens 4g..4g+3 of each of the two blocks) is exactly
+//           the B operand of O^T = V_hat^T P^T with those 8 tokens as its k-slots, so the A
+//           operand is the matching 4-byte words of the dimension-major V pages (one wave load
+//           covers 16 dimensions x 16 tokens of a page, contiguous), dequantized as
+//           bf16(fp32(code) * scale).  That operand does not depend on the rows: each wavefront
+//           dequantizes a quarter of the dimension tiles into LDS (two buffers, one barrier per
+//           stage) and reads all of them from there.  O^T accumulates in fp32 and leaves as
+//           BF16, four dimensions of one row per lane.
 // Rows are head-major (row r: head r / S, token r % S) as in the other kernels.  Row r sees
 // keys j <= T - S + r % S (the eager mask); T >= S is the caller's contract (the S new tokens
 // are part of the context), and a row that sees no key outputs 0.  The page ids of the
 // workgroup's blocks are staged in LDS, kPrefillWindow at a time.
-constexpr int kPrefillRows = 32;      // query rows per wavefront
-constexpr int kPrefillWaves = 4;      // wavefronts per workgroup
+// One MFMA row tile (16 rows) per wavefront: twice the wavefronts of two tiles, which pass 1
+// needs (2048 x 8192, 12/2/128: 296-311 -> 226-242 us); pass 2 then shares the dequantized V
+// of each stage through LDS (per wavefront it would cost twice the conversions: 588-604 us).
+constexpr int kPrefillRows = 16;   // query rows per wavefront (16 per MFMA row tile)
+constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
+// stages (two blocks each) in flight per wavefront: 3 measured equal, 4 slower (fewer resident
+// wavefronts in pass 2)
+constexpr int kPrefillRing = 2;
 constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
 
 template <int D, bool OUT>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a) {
-  constexpr int KK = D / 32, DT = D / 16, NT = 2;
+  constexpr int KK = D / 32, DT = D / 16, NT = kPrefillRows / 16;
+  constexpr int DTW = DT / kPrefillWaves;  // pass 2: dimension tiles of V each wavefront dequantizes
+  static_assert(DTW * kPrefillWaves == DT, "the wavefronts share the dimension tiles evenly");
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   __shared__ int lpb[kPrefillWindow];
   __shared__ int s_kend;
+  // pass 2: the dequantized V operand of a stage (it does not depend on the query rows, so the
+  // workgroup forms it once): [buffer][dimension tile][lane], 16 bytes each
+  __shared__ uint4 lv[OUT ? 2 : 1][OUT ? DT : 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int kvh = blockIdx.y, zb = blockIdx.z, b = zb % a.B, layer = zb / a.B;
   const int T = seq_len_of(a, b);
@@ -1641,8 +1654,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   }
   // blocks this wavefront streams (keys 0 .. max lim) and the smallest lim of its rows (every
   // key up to it is seen by every row: no mask inside a block below it)
-  int kend = max(lim[0], lim[1]) + 1;
-  int kmin = min(rv[0] ? lim[0] : INT_MAX, rv[1] ? lim[1] : INT_MAX);
+  int kend = 0, kmin = INT_MAX;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    kend = max(kend, lim[nt] + 1);
+    kmin = min(kmin, rv[nt] ? lim[nt] : INT_MAX);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     kend = max(kend, __shfl_xor(kend, off));
@@ -1682,10 +1699,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   }
 
   // A stage is two consecutive blocks u = 0, 1: K operands, page ids and, for pass 2, the V
-  // words (lane (g, n): dimension dt*16 + n, tokens 4g..4g+3) and the four scales of those tokens.
+  // words of this wavefront's dimension tiles wave*DTW .. (lane (g, n): dimension dt*16 + n,
+  // tokens 4g..4g+3) and the four scales of those tokens.
   struct Stage {
     bf16x8 k[2][KK];
-    uint32_t v[2][OUT ? DT : 1];
+    uint32_t v[2][OUT ? DTW : 1];
     float4 sc[2];
     int pb[2];
   };
@@ -1703,15 +1721,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int jb = 2 * s2 + u;
-        x.pb[u] = jb < jn ? lpb[jb] : -1;
+        x.pb[u] = jb < (OUT ? wn : jn) ? lpb[jb] : -1;
         const int64_t page = (int64_t)max(x.pb[u], 0) * a.KV + kvh;
         const uint16_t* kp = kbase + page * (kBlock * D);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) x.k[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + kk * 512));
         if constexpr (OUT) {
-          const uint8_t* vp = vlayer + (page * D + n) * kBlock + 4 * g;
+          const uint8_t* vp = vlayer + (page * D + wave * DTW * 16 + n) * kBlock + 4 * g;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) x.v[u][dt] = *reinterpret_cast<const uint32_t*>(vp + dt * 16 * kBlock);
+          for (int dtl = 0; dtl < DTW; ++dtl) x.v[u][dtl] = *reinterpret_cast<const uint32_t*>(vp + dtl * 16 * kBlock);
           x.sc[u] = *reinterpret_cast<const float4*>(slayer + page * kBlock + 4 * g);
         }
       }
@@ -1720,6 +1738,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       const int jg0 = w0 + 2 * s2;  // global block of u = 0
       bf16x8 pop[NT];
       uint32_t pw[NT][4];           // packed BF16 probabilities: u = 0 in words 0-1, u = 1 in 2-3
+      const bool mine = 2 * s2 < jn;  // wave-uniform: the stage has keys this wavefront's rows see
       // every key of the stage exists, is valid and is seen by every row: no mask
       const bool full = 2 * s2 + 1 < jn && x.pb[0] >= 0 && x.pb[1] >= 0 && (jg0 + 2) * kBlock - 1 <= kmin;
 #pragma unroll
@@ -1776,48 +1795,62 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       if constexpr (OUT) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[nt][0], pw[nt][1], pw[nt][2], pw[nt][3]));
-        // codes and scales of tokens that are not in the sequence (past T, invalid or absent
-        // blocks) become 0, so that no NaN pattern of an unwritten slot reaches the MFMA
-        if (!full) {
+        // this wavefront's dimension tiles of the stage's V operand, dequantized once for the
+        // workgroup.  Codes and scales of tokens that are not in the sequence (past T, invalid
+        // or absent blocks) become 0, so that no NaN pattern of an unwritten slot reaches the MFMA.
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int t0 = (jg0 + u) * kBlock + 4 * g;
-            const int nv = (2 * s2 + u < jn && x.pb[u] >= 0) ? min(max(T - t0, 0), 4) : 0;
-            const uint32_t mask = nv >= 4 ? 0xFFFFFFFFu : ((1u << (8 * nv)) - 1u);
+        for (int u = 0; u < 2; ++u) {
+          const int t0 = (jg0 + u) * kBlock + 4 * g;
+          const int nv = (2 * s2 + u < wn && x.pb[u] >= 0) ? min(max(T - t0, 0), 4) : 0;
+          if (nv < 4) {
+            const uint32_t mask = (1u << (8 * nv)) - 1u;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) x.v[u][dt] &= mask;
+            for (int dtl = 0; dtl < DTW; ++dtl) x.v[u][dtl] &= mask;
             x.sc[u].x = nv > 0 ? x.sc[u].x : 0.0f;
             x.sc[u].y = nv > 1 ? x.sc[u].y : 0.0f;
             x.sc[u].z = nv > 2 ? x.sc[u].z : 0.0f;
             x.sc[u].w = nv > 3 ? x.sc[u].w : 0.0f;
           }
         }
+        uint4 (*lvb)[64] = lv[s2 & 1];
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dt], false);
-          const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dt], true);
-          const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dt], false);
-          const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dt], true);
-          const bf16x8 vop = __builtin_bit_cast(
-              bf16x8, make_uint4(pack_bf16x2(f01.x * x.sc[0].x, f01.y * x.sc[0].y),
-                                 pack_bf16x2(f23.x * x.sc[0].z, f23.y * x.sc[0].w),
-                                 pack_bf16x2(f45.x * x.sc[1].x, f45.y * x.sc[1].y),
-                                 pack_bf16x2(f67.x * x.sc[1].z, f67.y * x.sc[1].w)));
+        for (int dtl = 0; dtl < DTW; ++dtl) {
+          const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dtl], false);
+          const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dtl], true);
+          const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dtl], false);
+          const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dtl], true);
+          lvb[wave * DTW + dtl][lane] =
+              make_uint4(pack_bf16x2(f01.x * x.sc[0].x, f01.y * x.sc[0].y), pack_bf16x2(f23.x * x.sc[0].z, f23.y * x.sc[0].w),
+                         pack_bf16x2(f45.x * x.sc[1].x, f45.y * x.sc[1].y), pack_bf16x2(f67.x * x.sc[1].z, f67.y * x.sc[1].w));
+        }
+        // every wavefront's tiles are in LDS; the other buffer is free again (its readers passed
+        // this barrier after their own reads of the previous stage)
+        __syncthreads();
+        if (mine) {
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dt][nt], 0, 0, 0);
+          for (int dt = 0; dt < DT; ++dt) {
+            const bf16x8 vop = __builtin_bit_cast(bf16x8, lvb[dt][lane]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dt][nt], 0, 0, 0);
+          }
         }
       }
     };
     // two stages in flight: one exit, at the loop head, and unconditional reloads (see the
-    // decode kernel: a break between the halves makes the compiler wait for every load)
-    const int nst = (jn + 1) >> 1;
-    Stage sa, sb;
-    load_stage(0, sa);
-    for (int s2 = 0; s2 < nst; s2 += 2) {
-      load_stage(s2 + 1, sb);
-      compute_stage(s2, sa);
-      load_stage(s2 + 2, sa);
-      if (s2 + 1 < nst) compute_stage(s2 + 1, sb);  // wave-uniform
+    // decode kernel: a break between the halves makes the compiler wait for every load).  Pass
+    // 2 runs every stage of the workgroup's window in every wavefront (each dequantizes its share
+    // of the V operand, with a barrier per stage); pass 1 only this wavefront's blocks.
+    const int nst = OUT ? ((wn + 1) >> 1) : ((jn + 1) >> 1);
+    Stage ring[kPrefillRing];
+#pragma unroll
+    for (int i = 0; i < kPrefillRing; ++i) load_stage(i, ring[i]);
+    for (int s2 = 0; s2 < nst; s2 += kPrefillRing) {
+#pragma unroll
+      for (int i = 0; i < kPrefillRing; ++i) {
+        const int ss = s2 + i;
+        if (ss < nst) compute_stage(ss, ring[i]);  // workgroup-uniform in pass 2, wave-uniform in pass 1
+        load_stage(ss + kPrefillRing, ring[i]);
+      }
     }
   }
 

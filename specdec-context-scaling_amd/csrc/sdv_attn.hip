@@ -1592,11 +1592,14 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // ---------------------------------------------------------------------------- prefill
 // Shapes with more query rows than one row-tile group holds (R = G*S > 64: prefill and
 // chunked-prefill blocks, model_self.py:471-504, 637-648) in two launches whose workspace holds
-// only the per-row (max, sum) -- 8 bytes per row -- instead of the O(S*T) scores:
-//   pass 1  each wavefront takes 16 rows (one MFMA row tile) and streams the page blocks its
-//           rows can see: S^T = K Q^T on MFMA (the K page is the A operand, the rows the B
-//           operand), scores rounded to BF16 twice, offset-causal mask, online (max, sum) per
-//           lane, merged over the lane groups into (M, L) per row.
+// only the per-row (max, sum) of each key part -- 32 bytes per row -- instead of the O(S*T)
+// scores:
+//   pass 1  each wavefront takes 16 rows (one MFMA row tile) and streams one of the
+//           kPrefillSplit parts of the page blocks its rows can see (one workgroup per part):
+//           S^T = K Q^T on MFMA (the K page is the A operand, the rows the B operand), scores
+//           rounded to BF16 twice, offset-causal mask, online (max, sum) per lane, merged over
+//           the lane groups into the part's (max, sum) per row; pass 2 merges the parts in
+//           part order into (M, L).
 //   pass 2  the workgroup streams the blocks of its rows again, two at a time; each wavefront
 //           recomputes its rows' BF16 scores and forms p = bf16(exp(s - M) / L) in registers.
 //           A lane's S^T fragment (row n, tokens 4g..4g+3 of each of the two blocks) is exactly
@@ -1619,6 +1622,10 @@ constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
 // stages (two blocks each) in flight per wavefront: 3 measured equal, 4 slower (fewer resident
 // wavefronts in pass 2)
 constexpr int kPrefillRing = 2;
+// Pass 1 splits each row group's keys in 4 parts, one workgroup each (four times the
+// wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1
+// 256 -> 163-175 us (12/2/128) and 218 -> 136-145 us (14/2/64); 2 parts 167-178 / 169-175 us
+constexpr int kPrefillSplit = 4;
 constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
 
 template <int D, bool OUT>
@@ -1636,7 +1643,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   const int kvh = blockIdx.y, zb = blockIdx.z, b = zb % a.B, layer = zb / a.B;
   const int T = seq_len_of(a, b);
   const int grp = zb * a.KV + kvh;
-  const int row0 = (blockIdx.x * kPrefillWaves + wave) * kPrefillRows;
+  // pass 1 splits the keys of a row group in kPrefillSplit parts, one workgroup each
+  const int split = OUT ? 0 : (int)(blockIdx.x % kPrefillSplit);
+  const int rgi = OUT ? (int)blockIdx.x : (int)(blockIdx.x / kPrefillSplit);
+  const int row0 = (rgi * kPrefillWaves + wave) * kPrefillRows;
 
   // this lane's rows (row tile nt: row row0 + nt*16 + n): q operand and last visible key
   bf16x8 qop[NT][KK];
@@ -1676,7 +1686,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
   const float* slayer = a.v_scales + layer * a.s_ls;
   const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
-  float2* st = a.stats + (int64_t)grp * a.R;
+  float2* st = a.stats + (int64_t)grp * a.R * kPrefillSplit;  // row r, part k: st[r * kPrefillSplit + k]
+  // this workgroup's key blocks: part `split` of [0, nblk_wg) (pass 2: all of them)
+  const int part = (((nblk_wg + kPrefillSplit - 1) / kPrefillSplit) + 1) & ~1;  // even: whole stages
+  const int blo = OUT ? 0 : min(nblk_wg, split * part);
+  const int bhi = OUT ? nblk_wg : min(nblk_wg, blo + part);
 
   float m_run[NT], l_run[NT], c_run[NT];   // pass 1: running max, sum and the sum's compensation
   float nml[NT], invl[NT];      // pass 2: -M log2 e and 1/L per row
@@ -1688,10 +1702,14 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     nml[nt] = 0.0f;
     invl[nt] = 0.0f;
     if (OUT && rv[nt]) {
-      const float2 v = st[row0 + nt * 16 + n];
-      if (v.y > 0.0f) {
-        nml[nt] = -v.x * kLog2e;
-        invl[nt] = 1.0f / v.y;
+      // (M, L) of the row: its parts merged in part order
+      const float2* sr = st + (int64_t)(row0 + nt * 16 + n) * kPrefillSplit;
+      float m = sr[0].x, l = sr[0].y;
+#pragma unroll
+      for (int k = 1; k < kPrefillSplit; ++k) merge_fast(m, l, sr[k].x, sr[k].y);
+      if (l > 0.0f) {
+        nml[nt] = -m * kLog2e;
+        invl[nt] = 1.0f / l;
       }
     }
 #pragma unroll
@@ -1707,8 +1725,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     float4 sc[2];
     int pb[2];
   };
-  for (int w0 = 0; w0 < nblk_wg; w0 += kPrefillWindow) {  // workgroup-uniform
-    const int wn = min(kPrefillWindow, nblk_wg - w0);
+  for (int w0 = blo; w0 < bhi; w0 += kPrefillWindow) {  // workgroup-uniform
+    const int wn = min(kPrefillWindow, bhi - w0);
     __syncthreads();  // the previous window's page ids are no longer read
     for (int j = tid; j < wn; j += 64 * kPrefillWaves) {
       const int pb = btrow[w0 + j];
@@ -1861,7 +1879,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       float m = m_run[nt], l = l_run[nt] + c_run[nt];
       merge_lanes<16>(m, l);
       merge_lanes<32>(m, l);
-      if (g == 0 && rv[nt]) st[row0 + nt * 16 + n] = make_float2(m, l);
+      if (g == 0 && rv[nt]) st[(int64_t)(row0 + nt * 16 + n) * kPrefillSplit + split] = make_float2(m, l);
     }
   } else {
     // lane (g, n) holds O[row nt*16 + n][dims dt*16 + 4g .. +3]
@@ -2171,7 +2189,7 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) only
     p->off_scores = p->off_partial = kSyncBytes;
     p->off_stats = kSyncBytes;
-    p->total = kSyncBytes + round_up((size_t)(groups * R * 8), 256);
+    p->total = kSyncBytes + round_up((size_t)(groups * R * 8 * kPrefillSplit), 256);
     return true;
   }
   // the sync area [0, kSyncBytes) is shared by every layout and only the fused kernel uses it
@@ -2320,7 +2338,8 @@ template <int D>
 static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
   if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
     const dim3 grid((unsigned)((a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves)), a.KV, zdim);
-    if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid, dim3(64 * kPrefillWaves), 0, st, a);
+    const dim3 grid1(grid.x * kPrefillSplit, grid.y, grid.z);
+    if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPrefillWaves), 0, st, a);
     if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid, dim3(64 * kPrefillWaves), 0, st, a);
     return;
   }

@@ -74,6 +74,8 @@ struct AttnArgs {
   // replays reuse it) and the bound of every cross-workgroup wait, in polls
   uint32_t tag;
   uint32_t spin_limit;
+  // prefill pass 2: key parts per row group (1: each workgroup writes its rows' outputs itself)
+  int pf_parts;
 };
 
 __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
@@ -1626,6 +1628,10 @@ constexpr int kPrefillRing = 2;
 // wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1
 // 256 -> 163-175 us (12/2/128) and 218 -> 136-145 us (14/2/64); 2 parts 167-178 / 169-175 us
 constexpr int kPrefillSplit = 4;
+// Pass 2: workgroups per row group (key parts; the last part to finish sums them).  Two for
+// head_dim 64 (2048 x 8192, 14/2/64: pass 2 277 -> 221 us); head_dim 128 keeps one (its pass 2
+// holds too many registers for more resident wavefronts: 368 -> 374-391 us with 2 or 4 parts)
+constexpr int prefill_parts(int D) { return D == 64 ? 2 : 1; }
 constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
 
 template <int D, bool OUT>
@@ -1643,9 +1649,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   const int kvh = blockIdx.y, zb = blockIdx.z, b = zb % a.B, layer = zb / a.B;
   const int T = seq_len_of(a, b);
   const int grp = zb * a.KV + kvh;
-  // pass 1 splits the keys of a row group in kPrefillSplit parts, one workgroup each
-  const int split = OUT ? 0 : (int)(blockIdx.x % kPrefillSplit);
-  const int rgi = OUT ? (int)blockIdx.x : (int)(blockIdx.x / kPrefillSplit);
+  // the keys of a row group are split in parts, one workgroup each: kPrefillSplit in pass 1,
+  // a.pf_parts in pass 2
+  const int nparts = OUT ? a.pf_parts : kPrefillSplit;
+  const int split = (int)(blockIdx.x % nparts);
+  const int rgi = (int)(blockIdx.x / nparts);
   const int row0 = (rgi * kPrefillWaves + wave) * kPrefillRows;
 
   // this lane's rows (row tile nt: row row0 + nt*16 + n): q operand and last visible key
@@ -1687,10 +1695,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   const float* slayer = a.v_scales + layer * a.s_ls;
   const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
   float2* st = a.stats + (int64_t)grp * a.R * kPrefillSplit;  // row r, part k: st[r * kPrefillSplit + k]
-  // this workgroup's key blocks: part `split` of [0, nblk_wg) (pass 2: all of them)
-  const int part = (((nblk_wg + kPrefillSplit - 1) / kPrefillSplit) + 1) & ~1;  // even: whole stages
-  const int blo = OUT ? 0 : min(nblk_wg, split * part);
-  const int bhi = OUT ? nblk_wg : min(nblk_wg, blo + part);
+  // this workgroup's key blocks: part `split` of [0, nblk_wg)
+  const int part = (((nblk_wg + nparts - 1) / nparts) + 1) & ~1;  // even: whole stages
+  const int blo = min(nblk_wg, split * part);
+  const int bhi = min(nblk_wg, blo + part);
 
   float m_run[NT], l_run[NT], c_run[NT];   // pass 1: running max, sum and the sum's compensation
   float nml[NT], invl[NT];      // pass 2: -M log2 e and 1/L per row
@@ -1882,16 +1890,82 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       if (g == 0 && rv[nt]) st[(int64_t)(row0 + nt * 16 + n) * kPrefillSplit + split] = make_float2(m, l);
     }
   } else {
-    // lane (g, n) holds O[row nt*16 + n][dims dt*16 + 4g .. +3]
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      if (!rv[nt]) continue;
-      const int r = row0 + nt * 16 + n, hl = r / a.S, si = r % a.S;
-      uint16_t* op = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + 4 * g;
+    // lane (g, n) holds O^T[dims dt*16 + 4g .. +3][row nt*16 + n] of this part's keys
+    static_assert(NT == 1, "the part slots hold one row tile per wavefront");
+    bool write = true;
+    if (nparts > 1) {  // workgroup-uniform
+      // Every part writes its fp32 partial to its slot (device-scope stores), waits for them,
+      // and counts itself in the row group's counter -- a (call tag, count) word in the sync
+      // area, read as 0 when it carries another call's tag.  The part that completes the count
+      // sums the slots in part order (its own from registers), writes the output and zeroes the
+      // counter.  Nobody waits for anybody: the order of arrival changes who sums, not the sum.
+      const int nrg = (a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves);
+      const int64_t slot_f = (int64_t)kPrefillRows * kPrefillWaves * D;  // floats per part slot
+      float* slots = a.partial + ((int64_t)grp * nrg + rgi) * nparts * slot_f;
+      const int rl = wave * kPrefillRows + n;  // row within the row group
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<uint2*>(op + dt * 16) =
-            make_uint2(pack_bf16x2(acc[dt][nt][0], acc[dt][nt][1]), pack_bf16x2(acc[dt][nt][2], acc[dt][nt][3]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __hip_atomic_store(slots + split * slot_f + (int64_t)rl * D + dt * 16 + 4 * g + i, acc[dt][0][i],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      SDV_VMCNT0();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __syncthreads();
+      __shared__ int s_last;
+      if (tid == 0) {
+        uint64_t* ctr = reinterpret_cast<uint64_t*>(a.sync) + kSyncHeadBytes / 8 + (int64_t)grp * nrg + rgi;
+        uint64_t old = load_dev_u64(ctr);
+        uint32_t mine = 0;
+        for (;;) {  // compare-and-swap against the other parts of this row group only
+          const uint32_t cnt = (uint32_t)(old >> 32) == a.tag ? (uint32_t)old : 0u;
+          const uint64_t nw = ((uint64_t)a.tag << 32) | (cnt + 1u);
+          const uint64_t prev = atomicCAS(reinterpret_cast<unsigned long long*>(ctr), (unsigned long long)old,
+                                          (unsigned long long)nw);
+          if (prev == old) {
+            mine = cnt + 1u;
+            break;
+          }
+          old = prev;
+        }
+        const bool last = mine == (uint32_t)nparts;
+        if (last) store_dev_u64(ctr, 0);
+        s_last = last;
+      }
+      __syncthreads();
+      write = s_last;
+      if (write) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          f32x4 sum = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+          for (int k = 0; k < nparts; ++k) {
+            f32x4 v;
+            if (k == split) {
+              v = acc[dt][0];
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                v[i] = __hip_atomic_load(slots + k * slot_f + (int64_t)rl * D + dt * 16 + 4 * g + i, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sum += v;
+          }
+          acc[dt][0] = sum;
+        }
+      }
+    }
+    if (write) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        if (!rv[nt]) continue;
+        const int r = row0 + nt * 16 + n, hl = r / a.S, si = r % a.S;
+        uint16_t* op = a.out + layer * a.q_ls + b * a.q_sb + (int64_t)(kvh * a.G + hl) * a.q_sh + si * a.q_ss + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          *reinterpret_cast<uint2*>(op + dt * 16) =
+              make_uint2(pack_bf16x2(acc[dt][nt][0], acc[dt][nt][1]), pack_bf16x2(acc[dt][nt][2], acc[dt][nt][3]));
+      }
     }
   }
 }
@@ -2147,6 +2221,7 @@ struct Plan {
   int64_t groups;
   bool group;                                     // group_kernel serves the call (many one-tile groups)
   int tpad;                                       // group_kernel: scratch row length (tokens)
+  int pf_parts;                                   // prefill pass 2: key parts per row group
   size_t total;                                   // bytes for every layout the call may take
 };
 
@@ -2186,10 +2261,20 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->groups = groups;
   p->group = false;
   p->tpad = 0;
-  if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) only
-    p->off_scores = p->off_partial = kSyncBytes;
+  p->pf_parts = 1;
+  if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) of each key part
+    p->off_scores = kSyncBytes;
     p->off_stats = kSyncBytes;
-    p->total = kSyncBytes + round_up((size_t)(groups * R * 8 * kPrefillSplit), 256);
+    const size_t stats = round_up((size_t)(groups * R * 8 * kPrefillSplit), 256);
+    p->off_partial = p->off_stats + stats;
+    // pass 2 splits the keys too when its counters (one per row group) fit the sync area's
+    // statistics region; its part slots follow the statistics
+    const int64_t nrg = (R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves);
+    p->pf_parts = (prefill_parts(D) > 1 && groups * nrg <= (int64_t)(kSyncStatsBytes / 8)) ? prefill_parts(D) : 1;
+    const size_t parts = p->pf_parts > 1
+                             ? round_up((size_t)(groups * nrg * p->pf_parts * kPrefillRows * kPrefillWaves * D * 4), 256)
+                             : 0;
+    p->total = p->off_partial + parts;
     return true;
   }
   // the sync area [0, kSyncBytes) is shared by every layout and only the fused kernel uses it
@@ -2338,9 +2423,9 @@ template <int D>
 static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
   if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
     const dim3 grid((unsigned)((a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves)), a.KV, zdim);
-    const dim3 grid1(grid.x * kPrefillSplit, grid.y, grid.z);
+    const dim3 grid1(grid.x * kPrefillSplit, grid.y, grid.z), grid2(grid.x * a.pf_parts, grid.y, grid.z);
     if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPrefillWaves), 0, st, a);
-    if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid, dim3(64 * kPrefillWaves), 0, st, a);
+    if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid2, dim3(64 * kPrefillWaves), 0, st, a);
     return;
   }
   if (phases == SDV_PHASE_ALL) {
@@ -2489,6 +2574,7 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.pv_chunk_tokens = p.pv_chunk_tokens;
   a.n_pv_chunks = p.n_pv_chunks;
   a.score_stride = p.score_stride;
+  a.pf_parts = p.pf_parts;
   // RN(1/sqrt(D)): 1/sqrt(128) = 0.08838834764831845, 1/sqrt(64) = 0.125 exactly
   a.inv_sqrt_d = head_dim == 128 ? 0.08838834764831845f : 0.125f;
 

@@ -118,3 +118,51 @@ def test_prefill_deterministic(cuda_device):
     outs = [ops.paged_attention(q, kp, vp, vs, cache.block_table(), cache.seq_lens_tensor(), t) for _ in range(3)]
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def test_prefill_key_parts_repeat_and_replay(cuda_device):
+    """head_dim 64 splits pass 2's keys in two parts per row group, and the part that finishes
+    last sums them (a per-row-group counter that it zeroes again): repeated eager calls and the
+    replays of a recorded call -- which reuse one tag -- with eager calls between them are
+    bitwise equal, on a batch of two sequences (two counters per KV head)."""
+    announce("prefill D=64 key parts: repeats and graph replays")
+    g = wl.gen(740, cuda_device)
+    lens, s, h, kv, d = [3000, 1200], 300, 14, 2, 64
+    cache = PagedKVCache(kv, d, batch=2, num_blocks=sum(-(-x // 16) for x in lens) + 5, device=cuda_device,
+                         seed=741, growable=False)
+    cache.prefill(0, torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16),
+                  torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16), lens)
+    q = torch.randn((2, s, h, d), generator=g, device=cuda_device).to(torch.bfloat16)
+    kp, vp, vs = cache.layer(0)
+    bt, sl = cache.block_table(), cache.seq_lens_tensor()
+    ws = ops.new_workspace(cuda_device, ops.attention_workspace_bytes(1, 2, h, kv, s, d, max(lens)))
+
+    def call(out=None):
+        return ops.paged_attention(q, kp, vp, vs, bt, sl, max(lens), q_token_major=True, out=out, workspace_tensor=ws)
+
+    eager = [call() for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(eager[0], eager[1]) and torch.equal(eager[1], eager[2])
+    out = torch.empty_like(q)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call(out)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[0]), "a replay differs from the eager call"
+        again = call()
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager[0]), "an eager call after a replay differs"
+    for b, t in enumerate(lens):  # and the numbers are the eager path's
+        kc, vc, sc = cache.gather(0, b)
+        v_hat = oq.dequantize_kv_fp8(vc.cpu()[None], sc.cpu()[None], torch.bfloat16)
+        want = oatt.eager_attention(q[b:b + 1].transpose(1, 2).cpu(), kc.cpu()[None], v_hat)
+        assert_close(eager[0][b:b + 1].transpose(1, 2).cpu(), want, f"key parts b={b} T={t}")

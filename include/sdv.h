@@ -154,8 +154,9 @@ int sdv_attention_set_wait_limit(uint32_t polls);
 
 /*
  * Which path sdv_paged_attention takes for these sizes on the current device: the number of
- * workgroups of the single-launch kernel, or 0 for the three-launch path (several
- * query-row groups, or a problem the device cannot hold at once).  Queries the device's
+ * workgroups of the single-launch kernel, or 0 when another path serves the call (several
+ * query-row groups, or a problem the device cannot hold at once: the persistent per-group
+ * kernel for 1024 or more one-tile groups, else three launches).  Queries the device's
  * occupancy; no launch.  No counterpart in the reference.
  */
 int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch, int32_t q_heads, int32_t kv_heads,

@@ -197,7 +197,11 @@ int sdv_paged_attention(const void* q, const void* k_pages, const void* v_pages,
  * softmax, FP8-V dequant, partial p.V), SDV_PHASE_REDUCE (sum partials, BF16 out).  Calling
  * it with SDV_PHASE_QK, then SDV_PHASE_PV, then SDV_PHASE_REDUCE on one stream with one
  * workspace computes exactly what one sdv_paged_attention call computes; a timer can record
- * events between the calls.  No counterpart in the reference.
+ * events between the calls.  Batches of 1024 or more one-tile groups (layers x batch x
+ * kv_heads with q_heads/kv_heads*q_len <= 16, max_seq_len <= 65536), which the persistent
+ * per-group kernel serves in one launch, have no split: a mask other than SDV_PHASE_ALL
+ * returns SDV_ERR_UNSUPPORTED.
+ * No counterpart in the reference.
  */
 #define SDV_PHASE_QK 1
 #define SDV_PHASE_PV 2

@@ -2286,12 +2286,11 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->off_partial = p->off_stats + stats;
   // the fused kernel keeps its statistics and partials inside the sync area
   p->total = p->off_partial + partial;
-  // group_kernel (words 2-3 of the sync area, then R scratch rows per workgroup at
-  // off_scores); the three-launch layout stays valid for the profiling entry point
+  // group_kernel: words 2-3 of the sync area, then R score rows per workgroup at off_scores
+  // (the profiling split refuses these shapes, so the three-launch layout is not needed)
   p->group = p->NT == 1 && groups >= kGroupMinGroups && max_seq_len <= kGroupMaxBlocks * kBlock;
   p->tpad = p->group ? (int)round_up((size_t)max_seq_len, kBlock) : 0;
-  if (p->group)
-    p->total = std::max(p->total, kSyncBytes + round_up((size_t)kGroupGrid * R * p->tpad * 2, 256));
+  if (p->group) p->total = kSyncBytes + round_up((size_t)kGroupGrid * R * p->tpad * 2, 256);
   return true;
 }
 
@@ -2510,6 +2509,7 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   if (q_token_major != 0 && q_token_major != 1) return SDV_ERR_SHAPE;
   Plan p;
   if (!make_plan(num_layers, batch, q_heads, kv_heads, q_len, head_dim, max_seq_len, &p)) return SDV_ERR_SHAPE;
+  if (p.group && phase_mask != SDV_PHASE_ALL) return SDV_ERR_UNSUPPORTED;  // one launch: no split
   if ((int64_t)max_blocks_per_seq * kBlock < max_seq_len) return SDV_ERR_SHAPE;
   const int64_t k_page = (int64_t)num_blocks * kv_heads * kBlock * head_dim;
   const int64_t s_page = (int64_t)num_blocks * kv_heads * kBlock;

@@ -170,3 +170,19 @@ def test_phase_trace_stays_out_of_the_product_library(lib):
     assert tlib.sdv_phase_trace_read(None, 1) == _native.SDV_ERR_NULL
     buf = (ctypes.c_uint64 * 1)()
     assert tlib.sdv_phase_trace_read(buf, 1 << 40) == _native.SDV_ERR_SHAPE
+
+
+def test_group_shapes_workspace_and_no_split(lib):
+    """A batch of 1024 or more one-tile groups runs in one launch of the per-group kernel: its
+    workspace is the synchronisation prefix plus 256 score rows per query row of the longest
+    sequence, and the profiling split refuses it (before any launch)."""
+    L, B, H, KV, D, T = 28, 32, 12, 2, 128, 32768          # 1792 groups of 6 rows
+    need = lib.sdv_attention_workspace_size(L, B, H, KV, 1, D, T)
+    assert need == _native.SYNC_BYTES + 256 * (H // KV) * T * 2
+    assert lib.sdv_attention_workspace_size(L, 8, H, KV, 1, D, T) > need   # 448 groups: three launches
+
+    def phases(mask):
+        return lib.sdv_paged_attention_phases(P, P, P, P, 8, 1 << 30, 1 << 30, 1 << 30, P, T // 16, P, L, B, H,
+                                              KV, 1, D, T, 0, P, 1 << 40, P, N, mask)
+    for mask in (_native.PHASE_QK, _native.PHASE_PV, 4):
+        assert phases(mask) == _native.SDV_ERR_UNSUPPORTED

@@ -76,18 +76,19 @@ def test_noalloc_matches_workspace_entry_point(cuda_device):
     assert torch.equal(out3, ref1)
 
 
-def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device):
-    """A three-launch shape (more (layer, sequence, KV head) groups than the device holds at
-    once) whose workspace exceeds the scratch: rejected on the host, nothing written."""
-    announce("noalloc: oversize three-launch shape is rejected")
+@pytest.mark.parametrize("L,B,t,group", [(8, 32, 8192, False), (16, 32, 8192, True)])
+def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device, L, B, t, group):
+    """Shapes whose workspace exceeds the scratch are rejected on the host and write nothing:
+    512 groups (three launches: scores, statistics and partials of every group) and 1024 groups
+    (the per-group kernel: 256 score rows per query row of the longest sequence)."""
+    announce(f"noalloc: oversize shape L={L} B={B} T={t} rejected ({'per-group' if group else 'three-launch'})")
     lib = _native.load()
     h, kv, d = 12, 2, 128
-    for L, B, t in ((8, 32, 2048), (28, 32, 2048), (8, 64, 4096)):
-        need = lib.sdv_attention_workspace_size(L, B, h, kv, 1, d, t)
-        if lib.sdv_attention_single_launch(L, B, h, kv, 1, d, t) == 0 and need > _native.NOALLOC_MAX_WORKSPACE:
-            break
-    else:
-        pytest.fail("no tested shape needs more workspace than the scratch holds")
+    need = lib.sdv_attention_workspace_size(L, B, h, kv, 1, d, t)
+    assert lib.sdv_attention_single_launch(L, B, h, kv, 1, d, t) == 0
+    assert need > _native.NOALLOC_MAX_WORKSPACE
+    if group:
+        assert need == _native.SYNC_BYTES + 256 * (h // kv) * t * 2
     cache = PagedKVCache(kv, d, num_layers=L, batch=B, num_blocks=B * (t // 16) + 1, device=cuda_device,
                          growable=False)
     for b in range(B):
@@ -98,3 +99,59 @@ def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device):
     assert _noalloc(q, cache, t, out) == _native.SDV_ERR_WORKSPACE
     torch.cuda.synchronize()
     assert bool((out == 7.0).all()), "a rejected call must not write its output"
+
+
+def _batch_cache(dev, layers, kv, d, lens, seed):
+    g = wl.gen(seed, dev)
+    cache = PagedKVCache(kv, d, num_layers=layers, batch=len(lens), num_blocks=sum(-(-t // 16) for t in lens) + 5,
+                         device=dev, seed=seed, growable=False)
+    slots = None
+    for layer in range(layers):
+        k = torch.randn((sum(lens), kv, d), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((sum(lens), kv, d), generator=g, device=dev).to(torch.bfloat16)
+        slots = cache.prefill(layer, k, v, lens, slots)
+    return cache
+
+
+def test_noalloc_group_and_prefill_paths(cuda_device):
+    """The per-group kernel (a claim counter that its last workgroup resets) and the head_dim 64
+    prefill (a counter per row group that the last key part resets) through the scratch, in the
+    order group -> prefill -> smaller group -> prefill again: every call equals
+    sdv_paged_attention's output bit for bit."""
+    lib = _native.load()
+    g = wl.gen(920, cuda_device)
+
+    def ref(q, cache, t):
+        if q.dim() == 5:
+            return ops.paged_attention(q, cache.k_pages, cache.v_pages, cache.v_scales, cache.block_table(),
+                                       cache.seq_lens_tensor(), t)
+        kp, vp, vs = cache.layer(0)
+        return ops.paged_attention(q, kp, vp, vs, cache.block_table(), cache.seq_lens_tensor(), t)
+
+    def both(q, cache, t, what):
+        out = torch.empty_like(q)
+        assert _noalloc(q, cache, t, out) == _native.SDV_OK, what
+        want = ref(q, cache, t)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"{what}: noalloc differs from sdv_paged_attention"
+
+    announce("noalloc: per-group kernel, 28 layers x 19 ragged sequences (1064 groups)")
+    lens_a = wl.ragged_lengths(19, 200, 2048, seed=921)
+    big = _batch_cache(cuda_device, 28, 2, 128, lens_a, seed=922)
+    assert lib.sdv_attention_workspace_size(28, 19, 12, 2, 1, 128, max(lens_a)) <= _native.NOALLOC_MAX_WORKSPACE
+    qa = torch.randn((28, 19, 12, 1, 128), generator=g, device=cuda_device).to(torch.bfloat16)
+    both(qa, big, max(lens_a), "group 28x19")
+
+    announce("noalloc: prefill rows, 14/2/64, S=300 over T=3000 (key parts)")
+    pf = _cache(cuda_device, 1, 2, 64, 3000, seed=923)
+    qp = torch.randn((1, 14, 300, 64), generator=g, device=cuda_device).to(torch.bfloat16)
+    both(qp, pf, 3000, "prefill 300x3000")
+
+    announce("noalloc: per-group kernel, 16 layers x 32 sequences up to 700 tokens")
+    lens_b = wl.ragged_lengths(32, 1, 700, seed=924)
+    small = _batch_cache(cuda_device, 16, 2, 128, lens_b, seed=925)
+    qb = torch.randn((16, 32, 12, 1, 128), generator=g, device=cuda_device).to(torch.bfloat16)
+    both(qb, small, max(lens_b), "group 16x32")
+
+    announce("noalloc: prefill rows again")
+    both(qp, pf, 3000, "prefill again")

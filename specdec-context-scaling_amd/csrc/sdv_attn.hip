@@ -612,8 +612,8 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
 // (layer*batch, KV head) group.  Every group is cut into the same number of items of nearly
 // equal size (the kernel also takes f_base+1 items for the first f_extra groups, which the
 // planner no longer uses), so every busy CU streams the same number of bytes.  Inside a
-// workgroup the wavefronts claim page blocks from an LDS counter, so a wavefront the
-// scheduler favours takes more blocks and all finish together.  Per workgroup:
+// workgroup wavefront w takes blocks (and p.V units) w, w + W, ...: a fixed trip count lets
+// each streaming loop end without loads past its last block.  Per workgroup:
 //   1. q.k^T over the item's blocks: BF16 scores and per-block (max, sum) of every row into
 //      LDS; the item's (max, sum) -- merged over its blocks in block order, so it does not
 //      depend on which wavefront took which block -- published to device memory as words
@@ -766,7 +766,7 @@ __host__ __device__ constexpr int fused_ntg_wide(int D, int W, int NT) {
 }
 
 // dynamic LDS of a fused workgroup with items of up to `maxblk` blocks (byte offsets).  With
-// one row tile the p.V work is claimed in units and each unit's result gets an LDS slot
+// one row tile the p.V work is split in units and each unit's result gets an LDS slot
 // ([stage][R][D] floats); otherwise the parts of the static split ([parts][R][D]).
 struct FusedLds {
   int scores, bstats, pages, gstats, parts, red, total;
@@ -803,10 +803,9 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   // NTG: dimension-tile groups in p.V (static split)
   constexpr int DTW = DT / NTG;          // 16-dimension tiles per wavefront
   constexpr int TP = W / NTG;            // block parts in p.V
-  constexpr int P = 1;                   // page blocks per q.k^T claim
+  constexpr int P = 1;                   // page blocks per q.k^T stage
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   extern __shared__ uint4 smem_u4[];
-  __shared__ int s_next, s_next2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int item = blockIdx.x;
   SDV_PHASE(0);
@@ -866,8 +865,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   for (int o4 = tid; o4 < n4; o4 += NTHR)
     __builtin_amdgcn_raw_buffer_store_b128((u32x4_t){0u, 0u, 0u, 0u}, prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
 
-  constexpr bool kClaimPV = NT == 1;  // one row tile: p.V units claimed like q.k^T blocks
-  const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kClaimPV, NTG);
+  constexpr bool kUnitPV = NT == 1;  // one row tile: p.V in units spread over the wavefronts
+  const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kUnitPV, NTG);
   char* smem = reinterpret_cast<char*>(smem_u4);
   uint16_t* lsc = reinterpret_cast<uint16_t*>(smem + lay.scores);  // row r: scores of query row r
   const int lrow = a.f_maxblk * kBlock + 8;
@@ -878,7 +877,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     const int pb = btrow[blk_lo + j];
     lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
   }
-  if (tid == 0) s_next = s_next2 = s_fail = 0;
+  if (tid == 0) s_fail = 0;
   // the group's new tokens inside this item's blocks go into the pages first; the barrier
   // (workgroup-scope release and acquire) makes them visible to the loads below, and only
   // this workgroup reads these blocks
@@ -905,12 +904,6 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   }
   {
     const uint16_t* kbase = a.k_pages + layer * a.k_ls + (int64_t)lane * 8;
-    // claim P blocks; returns the first (wave-uniform), >= nbv when the item is exhausted
-    auto claim = [&]() -> int {
-      int j = 0;
-      if (lane == 0) j = atomicAdd(&s_next, P);
-      return __builtin_amdgcn_readfirstlane(j);
-    };
     auto load_stage = [&](int j0, bf16x8 (&kop)[P][KK], int (&pbs)[P]) {
 #pragma unroll
       for (int u = 0; u < P; ++u) {
@@ -966,24 +959,33 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         }
       }
     };
-    // Two claims in flight per wavefront.  The loop has one exit, at its head, and both
-    // stages are reloaded unconditionally (an exhausted claim reads block 0, an L2 hit), so
-    // every path into the head has the same loads pending.  A break between the stages
-    // would merge the other stage's pending loads into the head, and the compiler then
-    // waits there for all loads before the next claim (one block in flight instead of two).
+    // Wavefront w streams blocks w, w + W, ... (ns of them), two in flight: the loop body
+    // loads the next two blocks while it multiplies the current ones, and the last one or two
+    // are peeled after it, so every path into the loop head has exactly one block pending
+    // (the wait before each multiply is exact) and no load goes past the item.  Claiming
+    // blocks from an LDS counter instead needs a load of some block after the last claim to
+    // keep the waits exact, and the barrier below then waits for that load (one layer at 8K:
+    // 13.1 -> 12.8 us with the p.V units below done the same way).
     bf16x8 ka[P][KK], kb[P][KK];
     int pa[P], pbb[P];
-    int ja = claim();
-    load_stage(ja, ka, pa);
-    bool more = ja < nbv;
-    while (more) {
-      const int jb2 = claim();
-      load_stage(jb2, kb, pbb);
-      compute_stage(ka, pa, ja);
-      ja = claim();
-      load_stage(ja, ka, pa);
-      compute_stage(kb, pbb, jb2);  // nothing when jb2 >= nbv
-      more = ja < nbv;              // claims increase: ja < nbv implies jb2 < nbv
+    const int ns = wave < nbv ? (nbv - 1 - wave) / W + 1 : 0;  // blocks wave, wave + W, ...
+    if (ns > 0) {
+      load_stage(wave, ka, pa);
+      int s = 0;
+      while (s + 2 < ns) {
+        load_stage(wave + (s + 1) * W, kb, pbb);
+        compute_stage(ka, pa, wave + s * W);
+        load_stage(wave + (s + 2) * W, ka, pa);
+        compute_stage(kb, pbb, wave + (s + 1) * W);
+        s += 2;
+      }
+      if (s + 1 < ns) {
+        load_stage(wave + (s + 1) * W, kb, pbb);
+        compute_stage(ka, pa, wave + s * W);
+        compute_stage(kb, pbb, wave + (s + 1) * W);
+      } else {
+        compute_stage(ka, pa, wave + s * W);
+      }
     }
   }
   __syncthreads();
@@ -995,56 +997,72 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   SDV_PHASE(2);
   uint64_t* fs = sync_stats(a);
-  // the item's statistics of each row, merged in an order that does not depend on which
-  // wavefront took which block in q.k^T.  One row per wavefront (decode): lane l merges
-  // blocks l, l+64, ... in order, then a fixed xor tree over the 64 lanes.  More rows
-  // (verify): the wavefront owns rows wave, wave + W, ... (rpw of them) and gives each a group
-  // of lpr lanes, so all its rows go through one pass (lane sl of a group merges blocks sl,
-  // sl + lpr, ... in order, then a fixed xor tree inside the group).
+  // the item's statistics of each row, in an order that does not depend on which wavefront
+  // took which block in q.k^T: the row's max over the item's blocks first, then each block's
+  // sum rescaled once against it and added along a fixed tree (one exp per block and no
+  // branches, where a pairwise (max, sum) merge spends two exps and a branch per tree level).
+  // One row per wavefront (decode): lane l takes blocks l, l+64, ... in order, then a tree
+  // over the 64 lanes whose result lane 0 holds.  More rows (verify): the wavefront owns rows
+  // wave, wave + W, ... (rpw of them) and gives each a group of lpr lanes, so all its rows go
+  // through one pass (lane sl of a group takes blocks sl, sl + lpr, ... in order, then a tree
+  // inside the group whose result the group's first lane holds).
   auto publish_stat = [&](int row, float m, float l) {
     uint64_t* p = fs + 2 * ((int64_t)item * 64 + row);
     store_dev_u64(p, tagged(m, a.tag));
     store_dev_u64(p + 1, tagged(l, a.tag));
   };
+  // one block's sum rescaled to the row max M (an empty block adds 0)
+  auto rescaled = [&](float2 v, float M) { return v.x == -INFINITY ? 0.0f : v.y * fast_exp(v.x - M); };
   const int rpw = (a.R + W - 1) / W;  // <= 16: R <= 64 rows, W >= 4
   if (rpw == 1) {
     if (wave < a.R) {
-      float m = -INFINITY, l = 0.0f;
-      for (int j = lane; j < nbv; j += kWave) {
-        const float2 v = bst[j * a.R + wave];
-        merge_fast(m, l, v.x, v.y);
-      }
-      // a fixed tree whose result lane 0 holds: lane 0 takes lanes 1, 2, 4 and 8 (row shifts
-      // and quad permutes), then rows 16 and 32 apart.  Lanes >= nbv hold nothing, so the tree
-      // only needs to span the first nbv lanes (wave-uniform tests).
-      if (nbv > 1) merge_xor_low<1>(m, l);
-      if (nbv > 2) merge_xor_low<2>(m, l);
-      if (nbv > 4) merge_xor_low<4>(m, l);
-      if (nbv > 8) merge_xor_low<8>(m, l);
-      if (nbv > 16) merge_lanes<16>(m, l);
-      if (nbv > 32) merge_lanes<32>(m, l);
-      if (lane == 0) publish_stat(wave, m, l);
+      // lane 0 takes lanes 1, 2, 4 and 8 (row shifts and quad permutes), then rows 16 and 32
+      // apart.  Lanes >= nbv hold nothing, so the tree only spans the first nbv lanes
+      // (wave-uniform tests).
+      float m = -INFINITY;
+      for (int j = lane; j < nbv; j += kWave) m = fmaxf(m, bst[j * a.R + wave].x);
+      if (nbv > 1) m = fmaxf(m, lane_xor_low<1>(m));
+      if (nbv > 2) m = fmaxf(m, lane_xor_low<2>(m));
+      if (nbv > 4) m = fmaxf(m, lane_xor_low<4>(m));
+      if (nbv > 8) m = fmaxf(m, lane_xor_low<8>(m));
+      if (nbv > 16) { const float2 p2 = lane_pair<16>(m); m = fmaxf(p2.x, p2.y); }
+      if (nbv > 32) { const float2 p2 = lane_pair<32>(m); m = fmaxf(p2.x, p2.y); }
+      const float M = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));  // lane 0: the row max
+      float l = 0.0f;
+      for (int j = lane; j < nbv; j += kWave) l += rescaled(bst[j * a.R + wave], M);
+      if (nbv > 1) l += lane_xor_low<1>(l);
+      if (nbv > 2) l += lane_xor_low<2>(l);
+      if (nbv > 4) l += lane_xor_low<4>(l);
+      if (nbv > 8) l += lane_xor_low<8>(l);
+      if (nbv > 16) { const float2 p2 = lane_pair<16>(l); l = p2.x + p2.y; }
+      if (nbv > 32) { const float2 p2 = lane_pair<32>(l); l = p2.x + p2.y; }
+      if (lane == 0) publish_stat(wave, M, l);
     }
   } else {
     const int lpr = rpw <= 2 ? 32 : rpw <= 4 ? 16 : rpw <= 8 ? 8 : 4;
     const int sub = lane / lpr, sl = lane - sub * lpr;
     const int row = wave + W * sub;
     const bool act = sub < rpw && row < a.R;
-    float m = -INFINITY, l = 0.0f;
-    if (act) {
-      for (int j = sl; j < nbv; j += lpr) {
-        const float2 v = bst[j * a.R + row];
-        merge_fast(m, l, v.x, v.y);
-      }
-    }
     // the group leaders (sl = 0: lanes that are multiples of lpr) take lanes 1, 2, 4, 8 and 16
     // apart, as far as the group reaches (wave-uniform tests)
-    merge_xor_low<1>(m, l);
-    merge_xor_low<2>(m, l);
-    if (lpr > 4) merge_xor_low<4>(m, l);
-    if (lpr > 8) merge_xor_low<8>(m, l);
-    if (lpr > 16) merge_lanes<16>(m, l);
-    if (act && sl == 0) publish_stat(row, m, l);
+    float m = -INFINITY;
+    if (act)
+      for (int j = sl; j < nbv; j += lpr) m = fmaxf(m, bst[j * a.R + row].x);
+    m = fmaxf(m, lane_xor_low<1>(m));
+    m = fmaxf(m, lane_xor_low<2>(m));
+    if (lpr > 4) m = fmaxf(m, lane_xor_low<4>(m));
+    if (lpr > 8) m = fmaxf(m, lane_xor_low<8>(m));
+    if (lpr > 16) { const float2 p2 = lane_pair<16>(m); m = fmaxf(p2.x, p2.y); }
+    const float M = __shfl(m, lane - sl);  // the leader's max, to its group
+    float l = 0.0f;
+    if (act)
+      for (int j = sl; j < nbv; j += lpr) l += rescaled(bst[j * a.R + row], M);
+    l += lane_xor_low<1>(l);
+    l += lane_xor_low<2>(l);
+    if (lpr > 4) l += lane_xor_low<4>(l);
+    if (lpr > 8) l += lane_xor_low<8>(l);
+    if (lpr > 16) { const float2 p2 = lane_pair<16>(l); l = p2.x + p2.y; }
+    if (act && sl == 0) publish_stat(row, M, l);
   }
 
   SDV_PHASE(3);
@@ -1056,7 +1074,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   // the group's statistics: wavefront nt waits until all nvq items have published row tile nt, merges them
   // in a fixed order -- item slice j takes items j, j+nsl, ..., then a fixed tree -- and shares
   // (max, 1/sum) of each row through LDS, so every wavefront and workgroup of the group gets
-  // identical values.  The other wavefronts' V loads stay in flight across the barrier.  An
+  // identical values.  Every wavefront issues its first V loads before this wait (the
+  // barrier at its end waits for them: the fence of __syncthreads covers global loads).  An
   // expired wait leaves (NaN, NaN): every probability, partial and output of the group is NaN.
   // A graph-recorded call reads the poison word with its first poll: on a poisoned workspace
   // (an earlier graph-recorded call expired, so statistics words carrying a recorded tag may be
@@ -1073,17 +1092,18 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       const int nsl = narrow ? 8 : 4;                      // item slices
       const int rl = narrow ? (lane & 7) : n, sl = narrow ? (lane >> 3) : g;
       const int ne = (nvq - sl + nsl - 1) / nsl;           // items of this slice (<= PB)
-      const int ne_max = (nvq + nsl - 1) / nsl;            // wave-uniform loop bound
       {
         const int nt = wave;
         const int rr = nt * 16 + rl;
         const uint64_t* fp = fs + 2 * ((int64_t)item0 * 64 + (rr < a.R ? rr : 0));
         const uint64_t ready_word = (uint64_t)a.tag << 32;  // stands in for entries past the slice
-        float m = -INFINITY, l = 0.0f;
+        float mk[PB], lk[PB];
         const uint32_t poison =
             graph_call ? __hip_atomic_load(a.sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
         bool expired = false;
-        for (int k0 = 0; k0 < ne_max; k0 += PB) {
+        static_assert(kFusedGroupItems <= 4 * PB, "every slice's entries fit one poll round");
+        {
+          constexpr int k0 = 0;
           uint64_t em[PB], el[PB];
 #pragma unroll
           for (int k = 0; k < PB; ++k) {
@@ -1110,12 +1130,34 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
             }
           }
 #pragma unroll
-          for (int k = 0; k < PB; ++k)
-            if (k0 + k < ne) merge_fast(m, l, word_value(em[k]), word_value(el[k]));
+          for (int k = 0; k < PB; ++k) {
+            mk[k] = k0 + k < ne ? word_value(em[k]) : -INFINITY;
+            lk[k] = k0 + k < ne ? word_value(el[k]) : 0.0f;
+          }
         }
-        if (narrow) merge_xor_low<8>(m, l);  // slices 2j and 2j+1 (lanes with bit 3 clear)
-        merge_lanes<16>(m, l);
-        merge_lanes<32>(m, l);
+        // The row's max over all of the group's entries first (the lane tree of the sum below),
+        // then each entry rescaled once against it and the rescaled sums added along the same
+        // tree: one exp per entry and no branches, where a pairwise (max, sum) merge spends
+        // two exps and a branch per merge level (one layer at 8K: 12.8 -> 12.4 us; one-layer
+        // verify 16.3 -> 15.7 us)
+        float m = mk[0];
+#pragma unroll
+        for (int k = 1; k < PB; ++k) m = fmaxf(m, mk[k]);
+        if (narrow) m = fmaxf(m, lane_xor_low<8>(m));  // valid in the lanes with bit 3 clear
+        float2 pm = lane_pair<16>(m);
+        m = fmaxf(pm.x, pm.y);
+        pm = lane_pair<32>(m);
+        m = fmaxf(pm.x, pm.y);
+        if (narrow)  // lanes with bit 3 set take the row's max from lane - 8
+          m = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(m), __float_as_int(m), 0x118, 0xF, 0xF, false));
+        float l = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PB; ++k) l += mk[k] == -INFINITY ? 0.0f : lk[k] * fast_exp(mk[k] - m);
+        if (narrow) l += lane_xor_low<8>(l);
+        float2 pl = lane_pair<16>(l);
+        l = pl.x + pl.y;
+        pl = lane_pair<32>(l);
+        l = pl.x + pl.y;
         if (expired || poison != 0) {  // wave-uniform (the poll loop exits on a ballot)
           m = l = __builtin_nanf("");
           if (lane == 0) s_fail = 1;
@@ -1160,10 +1202,10 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   };
 
   float gm[NT], ginv[NT];
-  if constexpr (kClaimPV) {
-    // Units of (4 blocks, up to 4 dimension tiles), claimed from an LDS counter so that all
-    // wavefronts finish together.  Each unit's fp32 result goes to its own LDS slot and the
-    // slots are summed in stage order, so the partial does not depend on who took what.
+  if constexpr (kUnitPV) {
+    // Units of (4 blocks, up to 4 dimension tiles); wavefront w takes units w, w + W, ...
+    // Each unit's fp32 result goes to its own LDS slot and the slots are summed in stage
+    // order, so the partial does not depend on which wavefront took which unit.
     constexpr int UT = DT < 4 ? DT : 4;  // 16-dimension tiles per unit
     constexpr int NH = DT / UT;          // units per stage of 4 blocks
     const int nstage = (nbv + 3) >> 2;
@@ -1173,12 +1215,6 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       float scl;
       int nvalid;
     };
-    auto claim2 = [&]() -> int {
-      int j = 0;
-      if (lane == 0) j = atomicAdd(&s_next2, 1);
-      return __builtin_amdgcn_readfirstlane(j);
-    };
-    // a unit past the end reads block 0 (the wait counters stay exact) and is never computed
     auto load_u = [&](int u, Unit& x) {
       const int k = u / NH, hf = u - k * NH;
       const int jb = 4 * k + g;
@@ -1250,10 +1286,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
           *reinterpret_cast<f32x4*>(lparts + ((k * a.R + n) * D + hf * UT * 16 + t * 16 + 4 * g)) = acc[t];
       }
     };
-    // two units in flight per wavefront; one loop exit, at the head (as in q.k^T)
+    // two units in flight per wavefront, the last ones peeled (as in q.k^T); the first unit
+    // is loaded before the group statistics wait
     Unit ua, ub;
-    int u0 = claim2();
-    load_u(u0, ua);
+    const int nsu = wave < nunits ? (nunits - 1 - wave) / W + 1 : 0;  // units wave, wave + W, ...
+    if (nsu > 0) load_u(wave, ua);
     group_stats(gm, ginv);
     SDV_PHASE(4);
     // p formed once per (row, token) before the loop: a unit covers half the dimensions of
@@ -1261,15 +1298,22 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     // 37.2 us together with the single-exit loops)
     prob_pass();
     __syncthreads();
-    bool more = u0 < nunits;
-    while (more) {
-      const int u1 = claim2();
-      load_u(u1, ub);
-      compute_u(u0, ua);
-      u0 = claim2();
-      load_u(u0, ua);
-      if (u1 < nunits) compute_u(u1, ub);  // wave-uniform
-      more = u0 < nunits;
+    if (nsu > 0) {
+      int s = 0;
+      while (s + 2 < nsu) {
+        load_u(wave + (s + 1) * W, ub);
+        compute_u(wave + s * W, ua);
+        load_u(wave + (s + 2) * W, ua);
+        compute_u(wave + (s + 1) * W, ub);
+        s += 2;
+      }
+      if (s + 1 < nsu) {
+        load_u(wave + (s + 1) * W, ub);
+        compute_u(wave + s * W, ua);
+        compute_u(wave + (s + 1) * W, ub);
+      } else {
+        compute_u(wave + s * W, ua);
+      }
     }
     __syncthreads();
     SDV_PHASE(5);
@@ -1300,8 +1344,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       s.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
     };
     // kVStages stages of V in flight per wavefront (3 with wider tiles): a stage is only 1 KiB
-    // of codes per 16-dim tile, so a deep ring keeps enough bytes moving; loads past the end read block 0 (the
-    // wait counters stay exact) and are never computed
+    // of codes per 16-dim tile, so a deep ring keeps enough bytes moving
     constexpr int SD = DTW >= 2 ? 3 : kVStages;
     Stage ring[SD];
     // With items of kPollFirstMinBlocks blocks or more the polling wavefronts load their
@@ -1313,13 +1356,15 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     const bool poll_first = a.f_maxblk >= kPollFirstMinBlocks;  // workgroup-uniform
     if (!poll_first || wave >= NT) {  // wave-uniform
   #pragma unroll
-      for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
+      for (int i = 0; i < SD; ++i)
+        if (i < nstage) load_v(i, ring[i]);
     }
     group_stats(gm, ginv);
     SDV_PHASE(4);
     if (poll_first && wave < NT) {
   #pragma unroll
-      for (int i = 0; i < SD; ++i) load_v(i, ring[i]);
+      for (int i = 0; i < SD; ++i)
+        if (i < nstage) load_v(i, ring[i]);
     }
     prob_pass();
     __syncthreads();
@@ -1385,17 +1430,30 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         }
       }
     };
-    // one loop exit, at the head, and unconditional reloads: every path into the head has
-    // the ring's loads pending in ring order, so stage i waits only for its own loads (a
-    // break after stage i would reorder the pending loads of the merged paths and make the
-    // compiler wait for nearly the whole ring before stage 0)
-    for (int st0 = 0; st0 < nstage; st0 += SD) {
+    // Full rounds (every reload a stage of the part) in a loop with one exit, at the head:
+    // every path into the head has the ring's loads pending in ring order, so stage i waits
+    // only for its own loads (a break after stage i would reorder the pending loads of the
+    // merged paths and make the compiler wait for nearly the whole ring).  The last (up to
+    // 2 * SD - 1) stages follow the loop with no loads past the part, which the barrier after
+    // p.V would otherwise wait for (one-layer verify at 8K: 16.7 -> 16.3 us).
+    int st0 = 0;
+    for (; st0 + 2 * SD <= nstage; st0 += SD) {  // every reload is a stage of the part
   #pragma unroll
       for (int i = 0; i < SD; ++i) {
-        if (st0 + i < nstage) compute_v(st0 + i, ring[i]);  // wave-uniform
+        compute_v(st0 + i, ring[i]);
         load_v(st0 + i + SD, ring[i]);
       }
     }
+  #pragma unroll
+    for (int i = 0; i < SD; ++i) {
+      if (st0 + i < nstage) {  // wave-uniform
+        compute_v(st0 + i, ring[i]);
+        if (st0 + i + SD < nstage) load_v(st0 + i + SD, ring[i]);
+      }
+    }
+  #pragma unroll
+    for (int i = 0; i < SD; ++i)
+      if (st0 + SD + i < nstage) compute_v(st0 + SD + i, ring[i]);
 
     // lane (g, n) holds rows nt*16+n, dims tg*DTW*16 + dtw*16 + 4g .. +3; parts summed in order
     if (TP > 1) {

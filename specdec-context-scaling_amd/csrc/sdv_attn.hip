@@ -675,16 +675,26 @@ constexpr uint32_t kDefaultSpinLimit = 1u << 20;
 // thread 0 of each of the first kPhaseTraceGroups workgroups stamps the 100 MHz wall clock at
 // the phase boundaries 0..9 (start, table + append done, q.k^T done, statistics published,
 // group statistics read, p.V done, partial published, owner polls done, output written, end)
-// into its kPhaseSlots words; sdv_phase_trace_read copies the array to the host.  The product
-// library compiles the stamps away.
+// of fused_kernel into LDS and writes its kPhaseSlots words out at the end (a global store per
+// stamp would make the next barrier wait for it: __syncthreads waits for the wavefront's
+// outstanding stores); sdv_phase_trace_read copies the array to the host.  The product library
+// compiles the stamps away.
 constexpr int kPhaseSlots = 16;
 constexpr int kPhaseTraceGroups = 4096;
 #ifdef SDV_PHASE_TRACE
 __device__ unsigned long long phase_trace[kPhaseTraceGroups * kPhaseSlots];
+#define SDV_PHASE_DECL                                                                      \
+  __shared__ unsigned long long s_phase[kPhaseSlots];                                       \
+  if (threadIdx.x == 0)                                                                     \
+    for (int i_ = 0; i_ < kPhaseSlots; ++i_) s_phase[i_] = 0
 #define SDV_PHASE(k)                                                                        \
   do {                                                                                      \
+    if (threadIdx.x == 0) s_phase[(k)] = wall_clock64();                                    \
+  } while (0)
+#define SDV_PHASE_FLUSH()                                                                   \
+  do {                                                                                      \
     if (threadIdx.x == 0 && blockIdx.x < kPhaseTraceGroups)                                 \
-      phase_trace[blockIdx.x * kPhaseSlots + (k)] = wall_clock64();                         \
+      for (int i_ = 0; i_ < kPhaseSlots; ++i_) phase_trace[blockIdx.x * kPhaseSlots + i_] = s_phase[i_]; \
   } while (0)
 // group_kernel accumulates per workgroup: words 10-12 = wall-clock ticks in claim + setup, q.k^T
 // (with the statistics merge) and p.V (with the output); word 13 = groups done.
@@ -695,8 +705,14 @@ __device__ unsigned long long phase_trace[kPhaseTraceGroups * kPhaseSlots];
   } while (0)
 #define SDV_CLOCK() wall_clock64()
 #else
+#define SDV_PHASE_DECL \
+  do {                 \
+  } while (0)
 #define SDV_PHASE(k) \
   do {               \
+  } while (0)
+#define SDV_PHASE_FLUSH() \
+  do {                    \
   } while (0)
 #define SDV_PHASE_ADD(k, v) \
   do {                      \
@@ -808,6 +824,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   extern __shared__ uint4 smem_u4[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int item = blockIdx.x;
+  SDV_PHASE_DECL;
   SDV_PHASE(0);
   const int big = a.f_extra * (a.f_base + 1);  // workgroups of the groups with one more item
   int grp, c, n_g, item0;
@@ -1075,7 +1092,9 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   // in a fixed order -- item slice j takes items j, j+nsl, ..., then a fixed tree -- and shares
   // (max, 1/sum) of each row through LDS, so every wavefront and workgroup of the group gets
   // identical values.  Every wavefront issues its first V loads before this wait (the
-  // barrier at its end waits for them: the fence of __syncthreads covers global loads).  An
+  // barrier at its end waits for them: the fence of __syncthreads covers global loads; an
+  // LDS-only barrier there, letting them run under the probability pass, measured no faster,
+  // as they have landed before the poll returns).  An
   // expired wait leaves (NaN, NaN): every probability, partial and output of the group is NaN.
   // A graph-recorded call reads the poison word with its first poll: on a poisoned workspace
   // (an earlier graph-recorded call expired, so statistics words carrying a recorded tag may be
@@ -1642,6 +1661,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     }
   }
   SDV_PHASE(9);
+  SDV_PHASE_FLUSH();
 }
 
 

@@ -822,6 +822,17 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int item = blockIdx.x;
   SDV_PHASE_DECL;
   SDV_PHASE(0);
+  {
+    // one field of each 64-byte line of the arguments, loaded together: the compiler fetches
+    // the arguments where they are first used, and each first touch of a line is a
+    // scalar-cache miss that the prologue would wait for in turn (one layer at 8K: 11.56 ->
+    // 11.08 us; the empty asm only makes the values live here)
+    const uint64_t l0 = (uint64_t)a.q;
+    const int l1 = a.f_base, l2 = a.max_seq_len;
+    const float l3 = a.inv_sqrt_d;
+    const uint32_t l4 = a.tag;
+    asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3), "s"(l4));
+  }
   const int big = a.f_extra * (a.f_base + 1);  // workgroups of the groups with one more item
   int grp, c, n_g, item0;
   if (item < big) {
@@ -836,8 +847,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     c = item - big - q * n_g;
     item0 = big + q * n_g;
   }
-  const int blk_lo = (int)((int64_t)c * a.f_gb / n_g);
-  const int nbk = (int)((int64_t)(c + 1) * a.f_gb / n_g) - blk_lo;  // item blocks, 1..f_maxblk
+  // 32-bit products and quotients: a group has at most 32 items and (items of at most
+  // 160 KiB of LDS) fewer than 2^18 blocks, so they stay far below 2^31 (a 64-bit division
+  // is a long software sequence in a prologue every call waits for)
+  const int blk_lo = (int)((unsigned)(c * a.f_gb) / (unsigned)n_g);
+  const int nbk = (int)((unsigned)((c + 1) * a.f_gb) / (unsigned)n_g) - blk_lo;  // item blocks, 1..f_maxblk
   const int zb = grp / a.KV, kvh = grp - zb * a.KV, b = zb % a.B, layer = zb / a.B;
   const int T = seq_len_of(a, b);
   const int tok0 = blk_lo * kBlock;
@@ -853,7 +867,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int nblk_seq = (T + kBlock - 1) >> 4;
   const int nbv = min(nbk, nblk_seq - blk_lo);  // item blocks inside the sequence (>= 1)
   // non-empty items of the group: item i starts at block floor(i * gb / n_g)
-  const int nvq = min(n_g, (int)(((int64_t)nblk_seq * n_g + a.f_gb - 1) / a.f_gb));
+  const int nvq = min(n_g, (int)((unsigned)(nblk_seq * n_g + a.f_gb - 1) / (unsigned)a.f_gb));
   // Output slice of this workgroup: workgroup c < nvq of the group owns 16-byte output chunks
   // [lo, lo + w) (four outputs each); nown workgroups have a non-empty slice.
   const int n4 = a.R * D / 4;

@@ -674,7 +674,8 @@ constexpr uint32_t kDefaultSpinLimit = 1u << 20;
 // Phase timeline of the single launch, in builds with SDV_PHASE_TRACE only (libsdv_trace.so):
 // thread 0 of each of the first kPhaseTraceGroups workgroups stamps the 100 MHz wall clock at
 // the phase boundaries 0..9 (start, table + append done, q.k^T done, statistics published,
-// group statistics read, p.V done, partial published, owner polls done, output written, end)
+// group statistics read, p.V done, partial published, owner polls and output sums done,
+// output written, end)
 // of fused_kernel into LDS and writes its kPhaseSlots words out at the end (a global store per
 // stamp would make the next barrier wait for it: __syncthreads waits for the wavefront's
 // outstanding stores); sdv_phase_trace_read copies the array to the host.  The product library

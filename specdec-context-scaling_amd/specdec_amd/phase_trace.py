@@ -31,7 +31,7 @@ from .engine.paged_cache import PagedKVCache
 from .kernels import ops
 
 PHASES = ("start", "block table + append done", "q.k^T done", "statistics published",
-          "group statistics read", "p.V done", "partial published", "owner polls done",
+          "group statistics read", "p.V done", "partial published", "owner polls + output sums done",
           "output written", "end")
 SLOTS = 16          # stamp words per workgroup (kPhaseSlots)
 MAX_GROUPS = 4096   # workgroups traced (kPhaseTraceGroups)

@@ -225,18 +225,26 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
   // no register copies between stages, so a stage's wait covers only its own loads.
   bf16x8 ka[P][KK], kb[P][KK];
   int pa[P], pbb[P];
-  // The prefetch is unconditional (a stage past the end reads block 0, which every wave of
-  // the layer shares in L2, and is masked): conditional loads would make the wait counters
-  // at the loop head imprecise and serialize the pipeline.
-  // The loop has one exit, at its head, and reloads both buffers unconditionally, so every
-  // path into the head has the same loads pending (a break between the two halves would
-  // merge the other buffer's pending loads into the head and make the compiler wait there).
-  if (nb > 0) load_stage(0, ka, pa);
-  for (int j0 = 0; j0 < nb; j0 += 2 * P) {
-    load_stage(j0 + P, kb, pbb);
-    compute_stage(ka, pa, j0);
-    load_stage(j0 + 2 * P, ka, pa);
-    compute_stage(kb, pbb, j0 + P);  // nothing past nb
+  // The loop has one exit, at its head, and every path into the head has exactly one stage
+  // pending (a break between the two halves would merge the other buffer's pending loads
+  // into the head and make the compiler wait there); the last one or two stages are peeled
+  // after it, so no stage past the wavefront's blocks is loaded (the barrier below would
+  // wait for it).  The second block of a half-full last stage reads block 0 and is masked.
+  const int nstg = (nb + P - 1) / P;
+  if (nstg > 0) load_stage(0, ka, pa);
+  int sg = 0;
+  for (; sg + 2 < nstg; sg += 2) {
+    load_stage((sg + 1) * P, kb, pbb);
+    compute_stage(ka, pa, sg * P);
+    load_stage((sg + 2) * P, ka, pa);
+    compute_stage(kb, pbb, (sg + 1) * P);
+  }
+  if (sg + 1 < nstg) {
+    load_stage((sg + 1) * P, kb, pbb);
+    compute_stage(ka, pa, sg * P);
+    compute_stage(kb, pbb, (sg + 1) * P);
+  } else if (sg < nstg) {
+    compute_stage(ka, pa, sg * P);
   }
 
 #pragma unroll
@@ -460,9 +468,9 @@ __global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
   const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
   const float* slayer = a.v_scales + layer * a.s_ls;
 
-  // Stages 0 and 1 of V are in flight while the statistics are merged.  The prefetch is
-  // unconditional (a stage past the end reads block 0 and is never computed) so the wait
-  // counters stay exact.
+  // Stages 0 and 1 of V are in flight while the statistics are merged.  These two loads are
+  // unconditional (a stage past the end reads block 0 and is never computed), so the wait
+  // for the statistics, issued before them, does not wait for them.
   const int nst = (nb + 3) >> 2;
   PvStage<D, NT> sa, sb;
   pv_load<D, NT>(sa, a, 0, my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
@@ -489,13 +497,22 @@ __global__ __launch_bounds__(256) void pv_kernel(AttnArgs a) {
   // Ping-pong over stages.  A stage is "full" (no masking) when all 64 of its slots are
   // tokens of the sequence -- wave-uniform.
   const int full_stages = min(nb, max(0, (T >> 4) - blk0)) >> 2;
-  for (int st_i = 0; st_i < nst; st_i += 2) {
+  // Full rounds (both reloads stages of the wavefront) in the loop, the last one to three
+  // stages after it: no stage past the end is loaded there (the barrier below would wait
+  // for it).
+  int st_i = 0;
+  for (; st_i + 3 < nst; st_i += 2) {
     pv_compute<D, NT>(sa, acc, gm, ginv, T, st_i < full_stages, n);
-    if (st_i + 1 >= nst) break;
     pv_load<D, NT>(sa, a, 4 * (st_i + 2), my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
     pv_compute<D, NT>(sb, acc, gm, ginv, T, st_i + 1 < full_stages, n);
     pv_load<D, NT>(sb, a, 4 * (st_i + 3), my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
   }
+  if (st_i < nst) {
+    pv_compute<D, NT>(sa, acc, gm, ginv, T, st_i < full_stages, n);
+    if (st_i + 2 < nst) pv_load<D, NT>(sa, a, 4 * (st_i + 2), my_pb, nb, blk0, vlayer, slayer, srow0, srow_off, kvh, g, n);
+  }
+  if (st_i + 1 < nst) pv_compute<D, NT>(sb, acc, gm, ginv, T, st_i + 1 < full_stages, n);
+  if (st_i + 2 < nst) pv_compute<D, NT>(sa, acc, gm, ginv, T, st_i + 2 < full_stages, n);
 
   // lane (g, n) holds O^T[dims dt*16 + 4g .. +3][row n]; the 4 waves sum in LDS per row tile.
   float* dst = a.partial + ((int64_t)grp * a.n_pv_chunks + c) * a.R * D;

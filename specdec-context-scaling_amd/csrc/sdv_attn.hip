@@ -624,7 +624,7 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
 
 // ---------------------------------------------------------------------------- fused
 // One launch for the shapes whose whole grid fits the device at once (one query-row group:
-// decode and verify).  One workgroup per CU (W = 8 or 16 wavefronts for decode; 8 or 4 when
+// decode and verify).  One workgroup per CU (W = 8 wavefronts for one or two row tiles, 4 when
 // the row tiles need more registers), each owning one item: a run of page blocks of one
 // (layer*batch, KV head) group.  Every group is cut into the same number of items of nearly
 // equal size (the kernel also takes f_base+1 items for the first f_extra groups, which the
@@ -777,11 +777,12 @@ __device__ __forceinline__ float4 part_dec(u32x4_t w) {
 
 // wavefronts of the fused workgroup for NT row tiles.  With one row tile the workgroup is
 // alone on its CU; measured on gfx950, 8 wavefronts finish a D=128 call sooner than 16 (one
-// layer at T=2048: 12.6 us vs 13.7 us; 28 layers at 8K: equal within noise), while D=64
-// blocks are half the bytes and 16 wavefronts keep more of them in flight (24 layers at
-// 8K: 23.7 us vs 25.5 us).
+// layer at T=2048: 12.6 us vs 13.7 us; 28 layers at 8K: equal within noise), and since the
+// streaming loops stopped loading past their items also a D=64 call (24 layers at 8K:
+// 21.8 -> 21.5 us, at 2K 13.05 -> 12.5 us; one layer at 2K 8.97 -> 8.49 us; with the
+// counter-claimed loops 16 had been faster for D=64: 23.7 us against 25.5 us at 8K).
 template <int D, int NT>
-constexpr int fused_waves() { return NT == 1 ? (D == 128 ? 8 : 16) : NT == 2 ? 8 : 4; }
+constexpr int fused_waves() { return NT <= 2 ? 8 : 4; }
 constexpr int kVStages = 6;  // p.V stages in flight per wavefront (one 16-dimension tile each)
 // dimension-tile groups of the static p.V split (several row tiles): wavefront w takes the
 // 16-dimension tiles of group w % ntg for block part w / ntg

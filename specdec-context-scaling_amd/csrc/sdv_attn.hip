@@ -2444,13 +2444,14 @@ static bool try_fused_w(AttnArgs a, const Plan& p, hipStream_t st) {
   return true;
 }
 
-// D=64 with one row tile and an in-kernel append runs 16 wavefronts: the draft chain (5 steps x
-// 24 layers at 8K, append + attention per layer) takes 1275 us with 16 against 1343 us with 8,
-// while the same calls without the append are faster with 8 (two launches per layer: 1601 ->
-// 1551 us)
+// One row tile with an in-kernel append runs 16 wavefronts: the draft chain (D=64, 5 steps x 24
+// layers at 8K, append + attention per layer) takes 1275 us with 16 against 1343 us with 8,
+// and 5 x 28 D=128 decode steps 1710 against 1735 us, while the same calls without the append
+// are faster with 8 (draft chain in two launches per layer: 1601 -> 1551 us).  Two row tiles
+// keep 8 (the 28-layer verify step with its appends: 441 us, 493 us with 16).
 template <int D, int NT>
 static bool try_fused(AttnArgs a, const Plan& p, hipStream_t st) {
-  if constexpr (D == 64 && NT == 1)
+  if constexpr (NT == 1)
     if (a.app_v) return try_fused_w<D, NT, 16>(a, p, st);
   return try_fused_w<D, NT, fused_waves<D, NT>()>(a, p, st);
 }

@@ -1678,10 +1678,10 @@ constexpr int kPrefillRing = 2;
 // wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1
 // 256 -> 163-175 us (12/2/128) and 218 -> 136-145 us (14/2/64); 2 parts 167-178 / 169-175 us
 constexpr int kPrefillSplit = 4;
-// Pass 2: workgroups per row group (key parts; the last part to finish sums them).  Two for
-// head_dim 64 (2048 x 8192, 14/2/64: pass 2 277 -> 221 us); head_dim 128 keeps one (its pass 2
-// holds too many registers for more resident wavefronts: 368 -> 374-391 us with 2 or 4 parts)
-constexpr int prefill_parts(int D) { return D == 64 ? 2 : 1; }
+// Pass 2: workgroups per row group (key parts; the last part to finish sums them): two (2048 x
+// 8192, 14/2/64: pass 2 277 -> 221 us; 12/2/128 with its one-stage ring below: 354-372 ->
+// 297-317 us)
+constexpr int prefill_parts(int D) { return 2; }
 constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
 
 template <int D, bool OUT>
@@ -1917,15 +1917,18 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     // 2 runs every stage of the workgroup's window in every wavefront (each dequantizes its share
     // of the V operand, with a barrier per stage); pass 1 only this wavefront's blocks.
     const int nst = OUT ? ((wn + 1) >> 1) : ((jn + 1) >> 1);
-    Stage ring[kPrefillRing];
+    // pass 2 for head_dim 128 keeps one stage: 98 VGPRs + 36 AGPRs, three wavefronts per SIMD
+    // (two with two stages), which the two key parts fill
+    constexpr int RING = (OUT && D == 128) ? 1 : kPrefillRing;
+    Stage ring[RING];
 #pragma unroll
-    for (int i = 0; i < kPrefillRing; ++i) load_stage(i, ring[i]);
-    for (int s2 = 0; s2 < nst; s2 += kPrefillRing) {
+    for (int i = 0; i < RING; ++i) load_stage(i, ring[i]);
+    for (int s2 = 0; s2 < nst; s2 += RING) {
 #pragma unroll
-      for (int i = 0; i < kPrefillRing; ++i) {
+      for (int i = 0; i < RING; ++i) {
         const int ss = s2 + i;
         if (ss < nst) compute_stage(ss, ring[i]);  // workgroup-uniform in pass 2, wave-uniform in pass 1
-        load_stage(ss + kPrefillRing, ring[i]);
+        load_stage(ss + RING, ring[i]);
       }
     }
   }

@@ -806,14 +806,14 @@ __host__ __device__ constexpr int fused_ntg_wide(int D, int W, int NT) {
 struct FusedLds {
   int scores, bstats, pages, gstats, parts, total;
 };
-__host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool claim_pv, int ntg) {
+__host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, int W, bool unit_pv, int ntg) {
   const int tp = W / ntg;
   FusedLds l;
   l.scores = 0;                                                            // [R][16*maxblk + 8] bf16
   l.bstats = (l.scores + R * (maxblk * kBlock + 8) * 2 + 15) & ~15;        // [maxblk][R] float2
   l.pages = l.bstats + maxblk * R * 8;                                     // [maxblk] int
   l.gstats = (l.pages + maxblk * 4 + 15) & ~15;                           // [64] float2
-  if (claim_pv) {
+  if (unit_pv) {
     l.parts = l.gstats + 64 * 8;
     l.total = l.parts + (maxblk + 3) / 4 * R * D * 4;
   } else {
@@ -1912,10 +1912,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
         }
       }
     };
-    // two stages in flight: one exit, at the loop head, and unconditional reloads (see the
-    // decode kernel: a break between the halves makes the compiler wait for every load).  Pass
-    // 2 runs every stage of the workgroup's window in every wavefront (each dequantizes its share
-    // of the V operand, with a barrier per stage); pass 1 only this wavefront's blocks.
+    // RING stages in flight: one exit, at the loop head, and unconditional reloads (a break
+    // between the stages would make the compiler wait for every load at the head; a reload
+    // past the window reads block 0 and is not computed).  Pass 2 runs every stage of the
+    // workgroup's window in every wavefront (each dequantizes its share of the V operand, with
+    // a barrier per stage); pass 1 only this wavefront's blocks.
     const int nst = OUT ? ((wn + 1) >> 1) : ((jn + 1) >> 1);
     // pass 2 for head_dim 128 keeps one stage: 98 VGPRs + 36 AGPRs, three wavefronts per SIMD
     // (two with two stages), which the two key parts fill

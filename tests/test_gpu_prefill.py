@@ -120,14 +120,15 @@ def test_prefill_deterministic(cuda_device):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
-def test_prefill_key_parts_repeat_and_replay(cuda_device):
-    """head_dim 64 splits pass 2's keys in two parts per row group, and the part that finishes
-    last sums them (a per-row-group counter that it zeroes again): repeated eager calls and the
-    replays of a recorded call -- which reuse one tag -- with eager calls between them are
-    bitwise equal, on a batch of two sequences (two counters per KV head)."""
-    announce("prefill D=64 key parts: repeats and graph replays")
-    g = wl.gen(740, cuda_device)
-    lens, s, h, kv, d = [3000, 1200], 300, 14, 2, 64
+@pytest.mark.parametrize("h,d", [(14, 64), (12, 128)])
+def test_prefill_key_parts_repeat_and_replay(cuda_device, h, d):
+    """Pass 2 splits each row group's keys in two parts, and the part that finishes last sums
+    them (a per-row-group counter that it zeroes again): repeated eager calls and the replays
+    of a recorded call -- which reuse one tag -- with eager calls between them are bitwise
+    equal, on a batch of two sequences (two counters per KV head)."""
+    announce(f"prefill {h}/2/{d} key parts: repeats and graph replays")
+    g = wl.gen(740 + d, cuda_device)
+    lens, s, kv = [3000, 1200], 300, 2
     cache = PagedKVCache(kv, d, batch=2, num_blocks=sum(-(-x // 16) for x in lens) + 5, device=cuda_device,
                          seed=741, growable=False)
     cache.prefill(0, torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16),

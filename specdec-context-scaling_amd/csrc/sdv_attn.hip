@@ -638,8 +638,9 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
 //   2. Once every item of the group has published (one wavefront polls, the others keep
 //      their first V loads in flight), the group's statistics are merged in a
 //      fixed order; the item's scores in LDS become p = bf16(exp(s - M) / L) in place, once
-//      per (row, token); the wavefronts run p.V over the item's blocks; per-unit results
-//      are summed in LDS in order and the fp32 partial is published.
+//      per (row, token); the wavefronts run p.V over the item's blocks, each summing its
+//      units in registers; the wavefronts' sums are added in LDS in wavefront order and the
+//      fp32 partial is published.
 //   3. Workgroup c of the group owns a slice of the outputs: it polls the slice of every
 //      item's partial, sums it over the items in order (the result does not depend on the
 //      order workgroups finish) into the BF16 output, and clears a share of the statistics
@@ -813,9 +814,9 @@ __host__ __device__ inline FusedLds fused_lds_layout(int R, int D, int maxblk, i
   l.bstats = (l.scores + R * (maxblk * kBlock + 8) * 2 + 15) & ~15;        // [maxblk][R] float2
   l.pages = l.bstats + maxblk * R * 8;                                     // [maxblk] int
   l.gstats = (l.pages + maxblk * 4 + 15) & ~15;                           // [64] float2
-  if (unit_pv) {
+  if (unit_pv) {  // one slot of R rows x (up to) 64 dimensions per wavefront
     l.parts = l.gstats + 64 * 8;
-    l.total = l.parts + (maxblk + 3) / 4 * R * D * 4;
+    l.total = l.parts + W * R * (D < 64 ? D : 64) * 4;
   } else {
     // the static split's parts are written after every wavefront has finished p.V: they
     // reuse the scores from offset 0
@@ -1251,11 +1252,15 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
 
   float gm[NT], ginv[NT];
   if constexpr (kUnitPV) {
-    // Units of (4 blocks, up to 4 dimension tiles); wavefront w takes units w, w + W, ...
-    // Each unit's fp32 result goes to its own LDS slot and the slots are summed in stage
-    // order, so the partial does not depend on which wavefront took which unit.
+    // Units of (4 blocks, up to 4 dimension tiles); wavefront w takes units w, w + W, ...,
+    // all of the same dimension tiles (W is a multiple of the units per stage), accumulates
+    // them in registers and leaves its sum in its own LDS slot; the item's partial adds the
+    // slots of each dimension tile in wavefront order.  The assignment is fixed, so the
+    // partial is bitwise repeatable.
     constexpr int UT = DT < 4 ? DT : 4;  // 16-dimension tiles per unit
     constexpr int NH = DT / UT;          // units per stage of 4 blocks
+    static_assert(W % NH == 0, "a wavefront's units cover the same dimension tiles");
+    constexpr int UD = UT * 16;          // dimensions of a unit (an LDS slot row)
     const int nstage = (nbv + 3) >> 2;
     const int nunits = nstage * NH;
     struct Unit {
@@ -1274,8 +1279,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       for (int t = 0; t < UT; ++t) x.code[t] = load_stream16(vp + t * 16 * kBlock);
       x.scl = __builtin_nontemporal_load(slayer + page * kBlock + n);
     };
+    f32x4 accw[UT];  // this wavefront's dimension tiles, summed over its units
+#pragma unroll
+    for (int t = 0; t < UT; ++t) accw[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     auto compute_u = [&](int u, Unit& x) {
-      const int k = u / NH, hf = u - k * NH;
+      const int k = u / NH;
       const int jb = 4 * k + g;
       if (__ballot(x.nvalid < kBlock) != 0) {  // wave-uniform: sanitize slots that are not tokens
         uint32_t bmask[4];
@@ -1293,9 +1301,6 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         }
         x.scl = n < x.nvalid ? x.scl : 0.0f;
       }
-      f32x4 acc[UT];
-#pragma unroll
-      for (int t = 0; t < UT; ++t) acc[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // the probabilities of the block (formed once in LDS); rows past R and lane groups
@@ -1324,14 +1329,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
           const bf16x8 vop = __builtin_bit_cast(
               bf16x8, make_uint4(pack_bf16x2(f01.x * sv[0], f01.y * sv[1]), pack_bf16x2(f23.x * sv[2], f23.y * sv[3]),
                                  pack_bf16x2(f45.x * sv[4], f45.y * sv[5]), pack_bf16x2(f67.x * sv[6], f67.y * sv[7])));
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, acc[t], 0, 0, 0);
+          accw[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, accw[t], 0, 0, 0);
         }
-      }
-      // lane (g, n) holds row n, dims hf*UT*16 + t*16 + 4g .. +3 of stage k
-      if (n < a.R) {
-#pragma unroll
-        for (int t = 0; t < UT; ++t)
-          *reinterpret_cast<f32x4*>(lparts + ((k * a.R + n) * D + hf * UT * 16 + t * 16 + 4 * g)) = acc[t];
       }
     };
     // two units in flight per wavefront, the last ones peeled (as in q.k^T); the first unit
@@ -1363,12 +1362,20 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
         compute_u(wave + s * W, ua);
       }
     }
+    // lane (g, n) holds row n, dims (wave % NH)*UD + t*16 + 4g .. +3; wavefronts w < nunits
+    // have units
+    if (nsu > 0 && n < a.R) {
+#pragma unroll
+      for (int t = 0; t < UT; ++t) *reinterpret_cast<f32x4*>(lparts + ((wave * a.R + n) * UD + t * 16 + 4 * g)) = accw[t];
+    }
     __syncthreads();
     SDV_PHASE(5);
-    // the item's partial: unit slots summed in stage order
+    // the item's partial: the slots of each dimension tile's wavefronts summed in wavefront order
+    const int wu = min(W, nunits);  // wavefronts with units
     for (int o4 = tid; o4 * 4 < a.R * D; o4 += NTHR) {
+      const int row = (4 * o4) / D, d = 4 * o4 - row * D, hf = d / UD, dl = d - hf * UD;
       f32x4 v = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-      for (int k = 0; k < nstage; ++k) v += *reinterpret_cast<const f32x4*>(lparts + k * a.R * D + 4 * o4);
+      for (int w = hf; w < wu; w += NH) v += *reinterpret_cast<const f32x4*>(lparts + ((w * a.R + row) * UD + dl));
       __builtin_amdgcn_raw_buffer_store_b128(part_enc(v), prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
     }
   } else {

@@ -310,6 +310,21 @@ def test_single_launch_odd_groups_and_ragged(cuda_device, layers, kv, h, lens):
                        f"L={layers} lens={lens}", seed=541)
 
 
+@pytest.mark.parametrize("d,h", [(128, 12), (64, 14)])
+def test_single_launch_large_items_batch32(cuda_device, d, h):
+    """One layer of a 32-sequence ragged batch of 2K-32K tokens (config 4's per-layer call) in
+    one launch: 64 groups whose items span up to 512 page blocks (each wavefront sums its p.V
+    units in registers).  Checked on the longest, the shortest, the first and the last sequence."""
+    lens = wl.ragged_lengths(32, 2048, 32768, seed=41)
+    announce(f"attn single launch B=32 ragged one layer {h}/2/{d} max T={max(lens)}")
+    grid = ops.single_launch_workgroups(1, 32, h, 2, 1, d, max(lens))
+    assert grid > 0 and grid % 64 == 0
+    assert -(-max(lens) // 16) // (grid // 64) >= 256  # blocks per item
+    cache = _filled_cache(cuda_device, 1, 2, d, lens, seed=575 + d)
+    seqs = tuple(sorted({0, 31, int(np.argmax(lens)), int(np.argmin(lens))}))
+    _check_multi_layer(cuda_device, cache, h, 1, (0,), seqs, f"B=32 ragged d={d}", seed=576)
+
+
 @pytest.mark.parametrize("t", [2048, 8192])
 def test_multi_layer_verify_s5(cuda_device, t):
     """The k+1=5-row verify over all 28 target layers in one launch."""

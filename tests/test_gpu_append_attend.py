@@ -3,8 +3,8 @@ call must leave the same bytes in the pages and give the same output as sdv_quan
 followed by sdv_paged_attention (model_self.py:697-706 then 739-776, one layer forward).
 
 Both sides run on the GPU from identical caches; the comparison is bitwise, for the single
-launch (each workgroup writes the new tokens of its own page blocks) and for the three-launch
-fallback (the append kernel runs first).  The attention itself is checked against the eager
+launch (each workgroup writes the new tokens of its own page blocks) and for the calls whose
+attention runs in other kernels (the append kernel runs first).  The attention itself is checked against the eager
 oracle by tests/test_gpu_attention.py.
 """
 from __future__ import annotations
@@ -45,7 +45,7 @@ def _same_pages(a, b):
     (12, 2, 128, [2046], 5),            # verify: positions 2046..2050 straddle blocks 127 / 128
     (14, 2, 64, [4095], 1),             # draft shape (D=64, 16 wavefronts)
     (12, 2, 128, [700, 33, 2047], 1),   # ragged batch
-    (12, 2, 128, [300, 1000], 16),      # 96 query rows: the three-launch path, append kernel first
+    (12, 2, 128, [300, 1000], 16),      # 96 query rows: the prefill kernels, append kernel first
 ])
 def test_append_attend_matches_append_then_attend(cuda_device, h, kv, d, lens, s):
     announce(f"append+attend h={h} kv={kv} d={d} lens={lens} s={s}")

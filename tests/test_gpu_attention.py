@@ -14,15 +14,16 @@ import torch
 from conftest import GOLDEN, announce
 from helpers import assert_close, bits16, build_pages, eager_ref, to_dev
 from oracle import attention as oatt
-from specdec_amd import workloads as wl
+from specdec_amd import _native, workloads as wl
 from specdec_amd.engine.paged_cache import PagedKVCache
 from specdec_amd.kernels import ops
 
 pytestmark = pytest.mark.gpu
 
 
-def _run_case(dev, h, kv, d, lens, s, *, seed, fragmented=True, extra_blocks=7, q_token_major=False):
-    """Random q/k/v per sequence, oracle-built pages, one kernel call; returns (got, want)."""
+def _run_case(dev, h, kv, d, lens, s, *, seed, fragmented=True, extra_blocks=7, q_token_major=False, split=False):
+    """Random q/k/v per sequence, oracle-built pages, one kernel call (split: the three launches
+    called one at a time on one workspace, the profiling split); returns (got, want)."""
     g = wl.gen(seed)
     B = len(lens)
     nbs = [-(-t // 16) for t in lens]
@@ -42,9 +43,15 @@ def _run_case(dev, h, kv, d, lens, s, *, seed, fragmented=True, extra_blocks=7, 
         bt[b, :len(r)] = r
     q = torch.stack(qs)                                   # (B, H, S, D)
     qd = q.transpose(1, 2).contiguous() if q_token_major else q
-    out = ops.paged_attention(qd.to(dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(sp, dev),
-                              to_dev(bt, dev), to_dev(np.array(lens, dtype=np.int32), dev), max(lens),
-                              q_token_major=q_token_major)
+    args = (qd.to(dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(sp, dev), to_dev(bt, dev),
+            to_dev(np.array(lens, dtype=np.int32), dev), max(lens))
+    if split:
+        ws = ops.new_workspace(dev, ops.attention_workspace_bytes(1, B, h, kv, s, d, max(lens)))
+        out = torch.empty_like(args[0])
+        for ph in (_native.PHASE_QK, _native.PHASE_PV, _native.PHASE_REDUCE):
+            ops.paged_attention(*args, q_token_major=q_token_major, phases=ph, out=out, workspace_tensor=ws)
+    else:
+        out = ops.paged_attention(*args, q_token_major=q_token_major)
     torch.cuda.synchronize()
     if q_token_major:
         out = out.transpose(1, 2)
@@ -119,15 +126,29 @@ def test_token_major_q_layout(cuda_device):
     assert_close(got, want, "token-major")
 
 
-def test_config4_batch32_ragged(cuda_device):
-    """B=32, T_b ~ U{2048..32768}, fragmented pool: every sequence within the bar."""
-    announce("attn config4 B=32 ragged")
+@pytest.mark.parametrize("split", [False, True])
+def test_config4_batch32_ragged(cuda_device, split):
+    """B=32, T_b ~ U{2048..32768}, fragmented pool: every sequence within the bar, through the
+    single launch (items of up to 512 blocks) and through the three launches one at a time."""
+    announce(f"attn config4 B=32 ragged split={split}")
     lens = wl.ragged_lengths(32, 2048, 32768, seed=4)
-    got, want = _run_case(cuda_device, 12, 2, 128, lens, 1, seed=73)
+    got, want = _run_case(cuda_device, 12, 2, 128, lens, 1, seed=73, split=split)
     worst = 0.0
     for b, t in enumerate(lens):
         worst = max(worst, assert_close(got[b], want[b], f"b={b} T={t}")["rel_l2"])
     print("config4 worst rel_l2", worst)
+
+
+def test_three_launch_many_groups(cuda_device):
+    """More one-tile groups than the device holds at once but fewer than the per-group kernel
+    takes (160 sequences x 2 KV heads): the planner's three launches, every sequence checked."""
+    announce("attn three launches, 160 ragged sequences")
+    g = np.random.default_rng(77)
+    lens = [int(x) for x in g.integers(17, 3000, size=160)]
+    assert ops.single_launch_workgroups(1, len(lens), 12, 2, 1, 128, max(lens)) == 0
+    got, want = _run_case(cuda_device, 12, 2, 128, lens, 1, seed=78)
+    for b, t in enumerate(lens):
+        assert_close(got[b], want[b], f"b={b} T={t}")
 
 
 def test_deterministic_bitwise(cuda_device):

@@ -905,12 +905,8 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   };
   const bool graph_call = (a.tag & kTagGraph) != 0;
   __shared__ int s_fail;  // a wait of this workgroup expired (or a graph-recorded call was refused)
-  // this item's partial slot starts the call zeroed: the stores are issued first and have
-  // completed (vmcnt(0) after q.k^T) before the item publishes its statistics
   const int64_t pstride = (int64_t)a.R * D;  // floats per item
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(sync_parts(a), (short)0, (int)kSyncPartBytes, 0x00020000);
-  for (int o4 = tid; o4 < n4; o4 += NTHR)
-    __builtin_amdgcn_raw_buffer_store_b128((u32x4_t){0u, 0u, 0u, 0u}, prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
 
   constexpr bool kUnitPV = NT == 1;  // one row tile: p.V in units spread over the wavefronts
   const FusedLds lay = fused_lds_layout(a.R, D, a.f_maxblk, W, kUnitPV, NTG);
@@ -1016,8 +1012,14 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     bf16x8 ka[P][KK], kb[P][KK];
     int pa[P], pbb[P];
     const int ns = wave < nbv ? (nbv - 1 - wave) / W + 1 : 0;  // blocks wave, wave + W, ...
+    if (ns > 0) load_stage(wave, ka, pa);
+    // This item's partial slot starts the call zeroed: the stores go out behind the first K
+    // loads (a wait for those loads does not cover them) and have completed before the item
+    // publishes its statistics (the barrier and vmcnt(0) after q.k^T).  Issued before the
+    // block-table barrier, which waits for them, they cost one-layer calls about 0.5 us.
+    for (int o4 = tid; o4 < n4; o4 += NTHR)
+      __builtin_amdgcn_raw_buffer_store_b128((u32x4_t){0u, 0u, 0u, 0u}, prs, (int)((item * pstride + 4 * o4) * 4), 0, 16);
     if (ns > 0) {
-      load_stage(wave, ka, pa);
       int s = 0;
       while (s + 2 < ns) {
         load_stage(wave + (s + 1) * W, kb, pbb);
@@ -1037,8 +1039,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   }
   __syncthreads();
   // the zeroing stores of this item's partial slot have completed before its statistics are
-  // published (placed here, the wait only covers the last, unused q.k^T prefetch; after the
-  // block-table loads it cost one-layer calls 0.5 us)
+  // published
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   SDV_VMCNT0();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);

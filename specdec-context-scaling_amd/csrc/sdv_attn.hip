@@ -2399,9 +2399,10 @@ struct FusedShape {
   size_t lds;
 };
 
-// The single-launch shape: as many workgroups as the device holds at once (at most 64 items
-// per group, items of at least one page block), or false when the three-launch path must
-// serve the call (several query-row groups, too many groups, items too large for LDS).
+// The single-launch shape: as many workgroups as the device holds at once (at most
+// kFusedGroupItems items per group, items of at least one page block), or false when another
+// path must serve the call (several query-row groups, more groups than the device holds at
+// once, items too large for LDS).
 template <int D, int NT, int W>
 static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
   if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;

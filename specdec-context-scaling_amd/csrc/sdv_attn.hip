@@ -195,12 +195,14 @@ __global__ __launch_bounds__(256) void qk_kernel(AttnArgs a) {
       for (int nt = 0; nt < NT; ++nt) {
         float s4[4];
         float mt = -INFINITY;
+        // bf16(bf16(q.k) / sqrt(D)): for BF16 inputs, dividing by RN(sqrt(D)) and multiplying
+        // by RN(1/sqrt(D)) round to the same BF16 (checked for all inputs).
+        float y[4];
+        round_scaled4(acc[nt][0], acc[nt][1], acc[nt][2], acc[nt][3], a.inv_sqrt_d, y);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = tb + i;
-          // bf16(bf16(q.k) / sqrt(D)): for BF16 inputs, dividing by RN(sqrt(D)) and
-          // multiplying by RN(1/sqrt(D)) round to the same BF16 (checked for all inputs).
-          const float x = round_bf16(round_bf16(acc[nt][i]) * a.inv_sqrt_d);
+          const float x = y[i];
           const bool vis = blk_ok && t < T && t <= T - a.S + qsi[nt];
           s4[i] = vis ? x : -INFINITY;
           mt = fmaxf(mt, s4[i]);
@@ -970,10 +972,12 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
           for (int kk = 0; kk < KK; ++kk) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[u][kk], qop[nt][kk], acc, 0, 0, 0);
           float s4[4];
           float mt = -INFINITY;
+          float y[4];
+          round_scaled4(acc[0], acc[1], acc[2], acc[3], a.inv_sqrt_d, y);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int t = tb + i;
-            const float x = round_bf16(round_bf16(acc[i]) * a.inv_sqrt_d);
+            const float x = y[i];
             const bool vis = blk_ok && t < T && t <= T - a.S + qsi[nt];
             s4[i] = vis ? x : -INFINITY;
             mt = fmaxf(mt, s4[i]);
@@ -1854,9 +1858,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
 #pragma unroll
           for (int kk = 0; kk < KK; ++kk) sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.k[u][kk], qop[nt][kk], sacc, 0, 0, 0);
           float s4[4];
+          float y[4];
+          round_scaled4(sacc[0], sacc[1], sacc[2], sacc[3], a.inv_sqrt_d, y);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float v = round_bf16(round_bf16(sacc[i]) * a.inv_sqrt_d);
+            const float v = y[i];
             s4[i] = (full || (blk_ok && t0 + i <= lim[nt])) ? v : -INFINITY;
           }
           if constexpr (!OUT) {
@@ -2158,9 +2164,11 @@ __global__ __launch_bounds__(64 * kGroupWaves) void group_kernel(AttnArgs a, int
         const int tb = j * kBlock + 4 * g;  // this lane's first token
         float s4[4];
         float mt = -INFINITY;
+        float y[4];
+        round_scaled4(acc[0], acc[1], acc[2], acc[3], a.inv_sqrt_d, y);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float x = round_bf16(round_bf16(acc[i]) * a.inv_sqrt_d);
+          const float x = y[i];
           s4[i] = (pb >= 0 && tb + i <= lim) ? x : -INFINITY;
           mt = fmaxf(mt, s4[i]);
         }

@@ -1669,7 +1669,7 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // ---------------------------------------------------------------------------- prefill
 // Shapes with more query rows than one row-tile group holds (R = G*S > 64: prefill and
 // chunked-prefill blocks, model_self.py:471-504, 637-648) in two launches whose workspace holds
-// only the per-row (max, sum) of each key part -- 32 bytes per row -- instead of the O(S*T)
+// only the per-row (max, sum) of each key part -- 64 bytes per row -- instead of the O(S*T)
 // scores:
 //   pass 1  each wavefront takes 16 rows (one MFMA row tile) and streams one of the
 //           kPrefillSplit parts of the page blocks its rows can see (one workgroup per part):
@@ -1699,10 +1699,12 @@ constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
 // stages (two blocks each) in flight per wavefront: 3 measured equal, 4 slower (fewer resident
 // wavefronts in pass 2)
 constexpr int kPrefillRing = 2;
-// Pass 1 splits each row group's keys in 4 parts, one workgroup each (four times the
-// wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1
-// 256 -> 163-175 us (12/2/128) and 218 -> 136-145 us (14/2/64); 2 parts 167-178 / 169-175 us
-constexpr int kPrefillSplit = 4;
+// Pass 1 splits each row group's keys in 8 parts, one workgroup each (eight times the
+// wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1 with one
+// part 256 / 218 us (12/2/128 / 14/2/64), 2 parts 167-178 / 169-175, 4 parts 163-175 /
+// 136-146, 8 parts 160-172 / 120-129 us (the 4-part grid ran 1.5 rounds of resident
+// wavefronts, the 8-part grid runs 3)
+constexpr int kPrefillSplit = 8;
 // Pass 2: workgroups per row group (key parts; the last part to finish sums them): two (2048 x
 // 8192, 14/2/64: pass 2 277 -> 221 us; 12/2/128 with its one-stage ring below: 354-372 ->
 // 297-317 us)

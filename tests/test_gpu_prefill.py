@@ -4,8 +4,8 @@ Reference: the prefill chunk of model_self.py:637-648 (2048-token chunks) attend
 cache plus the chunk with the offset-causal keep-mask of model_self.py:471-479 (row i sees keys
 j <= T - S + i); its fused path (cuDNN SDPA, :491-504) exists to avoid the O(S*T) score tensor
 of the eager path (docs/data_ledger.md:1145-1152: 74.1 MiB transient at 12q/2048q/8192kv).
-Here the two prefill passes keep 32 bytes per query row in the workspace (a (max, sum) for
-each of four key parts); the numbers must still be the eager BF16 path's (max-abs 2e-2,
+Here the two prefill passes keep 64 bytes per query row in the workspace (a (max, sum) for
+each of eight key parts); the numbers must still be the eager BF16 path's (max-abs 2e-2,
 rel-L2 1e-3 per row block).  The oracle runs on the
 CPU in row chunks (row i of a chunk of rows [i0, i1) sees keys j <= T - S + i0 + i, the same
 mask), so its memory stays bounded.

@@ -53,7 +53,9 @@ struct AttnArgs {
   float2* stats;
   float* partial;
   unsigned* sync;   // fused path: expired-wait count, published statistics and partials (zero between calls)
-  int f_gb, f_base, f_extra, f_maxblk;  // fused: blocks per group, items per group (+1 for the first f_extra groups), LDS width
+  // fused: blocks per group, items per group, LDS width in blocks; f_layers > 0: items sized
+  // per sequence (a batch with per-sequence lengths, f_layers layers)
+  int f_gb, f_base, f_layers, f_maxblk;
   int64_t q_ls, q_sb, q_sh, q_ss;  // element strides of q/out: layer, batch, head, row
   int max_blocks, num_blocks, max_seq_len;
   int B, KV, S, G, R;
@@ -629,8 +631,8 @@ __device__ __forceinline__ void append_new_tokens(const AttnArgs& a, int layer, 
 // decode and verify).  One workgroup per CU (W = 8 wavefronts for one or two row tiles, 4 when
 // the row tiles need more registers), each owning one item: a run of page blocks of one
 // (layer*batch, KV head) group.  Every group is cut into the same number of items of nearly
-// equal size (the kernel also takes f_base+1 items for the first f_extra groups, which the
-// planner no longer uses), so every busy CU streams the same number of bytes.  Inside a
+// equal size, so every busy CU streams the same number of bytes (a batch with per-sequence
+// lengths sizes each sequence's items from its length instead: f_layers, below).  Inside a
 // workgroup wavefront w takes blocks (and p.V units) w, w + W, ...: a fixed trip count lets
 // each streaming loop end without loads past its last block.  Per workgroup:
 //   1. q.k^T over the item's blocks: BF16 scores and per-block (max, sum) of every row into
@@ -855,25 +857,75 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
     const uint32_t l4 = a.tag;
     asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3), "s"(l4));
   }
-  const int big = a.f_extra * (a.f_base + 1);  // workgroups of the groups with one more item
-  int grp, c, n_g, item0;
-  if (item < big) {
-    n_g = a.f_base + 1;
+  int grp, c, n_g, item0, gbg;  // group, item in it, its items, its first item, its blocks
+  if (a.f_layers > 0) {
+    // A batch with per-sequence lengths (at most 64 sequences, one per lane): the groups of
+    // sequence b get ceil(blocks_b / S) items -- at most kFusedGroupItems, at most one per
+    // block, one for an empty sequence -- with S the smallest item size whose items fit the
+    // grid, found by bisection over [1, f_maxblk] (S = f_maxblk fits: the host plan gives every
+    // group f_base items of at most f_maxblk blocks).  Long sequences are cut finer than short
+    // ones instead of every group getting the items of the longest, and no item exceeds
+    // f_maxblk blocks (LDS).  Every workgroup derives the same plan from seq_lens; workgroups
+    // past it exit.  Items of layer l, sequence b, KV head h start at
+    // l * KV * sum(items) + KV * prefix_b + h * items_b.
+    const int B = a.B, L = a.f_layers, gs = L * a.KV;  // groups per sequence
+    const int Tb = lane < B ? seq_len_of(a, lane) : 0;
+    const int blk = (Tb + kBlock - 1) >> 4;
+    auto items_for = [&](int sz) {  // sz: wave-uniform item size
+      return lane < B ? (Tb == 0 ? 1 : min(min(kFusedGroupItems, blk), (blk + sz - 1) / sz)) : 0;
+    };
+    auto wave_sum = [&](int v) {  // exact: at most 64 * 32 items
+      float f = (float)v;
+      f += lane_xor_low<1>(f);
+      f += lane_xor_low<2>(f);
+      f += lane_xor_low<4>(f);
+      f += lane_xor_low<8>(f);
+      float2 pr = lane_pair<16>(f);
+      f = pr.x + pr.y;
+      pr = lane_pair<32>(f);
+      f = pr.x + pr.y;
+      return (int)__int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(f)));  // lane 0 holds the sum
+    };
+    int lo = 1, hi = a.f_maxblk;
+    while (lo < hi) {  // wave-uniform
+      const int mid = (lo + hi) >> 1;
+      if (gs * wave_sum(items_for(mid)) <= (int)gridDim.x)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    const int items = items_for(lo);
+    int incl = items;  // inclusive prefix over the sequences
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int v = __shfl_up(incl, off);
+      if (lane >= off) incl += v;
+    }
+    const int per_layer = a.KV * __shfl(incl, kWave - 1);
+    const int li = item / per_layer;
+    if (li >= L) return;  // workgroup-uniform: past the plan
+    const int r = item - li * per_layer;
+    const int excl = incl - items;
+    const uint64_t mine = __ballot(lane < B && r >= a.KV * excl && r < a.KV * incl);
+    const int bs = __builtin_ctzll(mine);  // the sequence
+    n_g = __shfl(items, bs);
+    gbg = __shfl(blk, bs);
+    const int rr = r - a.KV * __shfl(excl, bs);
+    const int h = rr / n_g;
+    c = rr - h * n_g;
+    item0 = item - c;
+    grp = (li * B + bs) * a.KV + h;
+  } else {
+    n_g = a.f_base;
     grp = item / n_g;
     c = item - grp * n_g;
     item0 = grp * n_g;
-  } else {
-    n_g = a.f_base;
-    const int q = (item - big) / n_g;
-    grp = a.f_extra + q;
-    c = item - big - q * n_g;
-    item0 = big + q * n_g;
+    gbg = a.f_gb;
   }
   // 32-bit products and quotients: a group has at most 32 items and (items of at most
   // 160 KiB of LDS) fewer than 2^18 blocks, so they stay far below 2^31 (a 64-bit division
   // is a long software sequence in a prologue every call waits for)
-  const int blk_lo = (int)((unsigned)(c * a.f_gb) / (unsigned)n_g);
-  const int nbk = (int)((unsigned)((c + 1) * a.f_gb) / (unsigned)n_g) - blk_lo;  // item blocks, 1..f_maxblk
+  const int blk_lo = (int)((unsigned)(c * gbg) / (unsigned)n_g);
+  const int nbk = (int)((unsigned)((c + 1) * gbg) / (unsigned)n_g) - blk_lo;  // item blocks, 1..f_maxblk
   const int zb = grp / a.KV, kvh = grp - zb * a.KV, b = zb % a.B, layer = zb / a.B;
   const int T = seq_len_of(a, b);
   const int tok0 = blk_lo * kBlock;
@@ -889,7 +941,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
   const int nblk_seq = (T + kBlock - 1) >> 4;
   const int nbv = min(nbk, nblk_seq - blk_lo);  // item blocks inside the sequence (>= 1)
   // non-empty items of the group: item i starts at block floor(i * gb / n_g)
-  const int nvq = min(n_g, (int)((unsigned)(nblk_seq * n_g + a.f_gb - 1) / (unsigned)a.f_gb));
+  const int nvq = min(n_g, (int)((unsigned)(nblk_seq * n_g + gbg - 1) / (unsigned)gbg));
   // Output slice of this workgroup: workgroup c < nvq of the group owns 16-byte output chunks
   // [lo, lo + w) (four outputs each); nown workgroups have a non-empty slice.
   const int n4 = a.R * D / 4;
@@ -2412,16 +2464,17 @@ static int fused_capacity(size_t lds) {
 }
 
 struct FusedShape {
-  int gb, base, extra, maxblk, grid, ntg;
+  int gb, base, layers, maxblk, grid, ntg;
   size_t lds;
 };
 
 // The single-launch shape: as many workgroups as the device holds at once (at most
 // kFusedGroupItems items per group, items of at least one page block), or false when another
 // path must serve the call (several query-row groups, more groups than the device holds at
-// once, items too large for LDS).
+// once, items too large for LDS).  per_seq_layers > 0: a batch of 2..64 sequences with
+// per-sequence lengths over that many layers, whose items the kernel sizes per sequence.
 template <int D, int NT, int W>
-static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
+static bool fused_shape(const Plan& p, int R, int max_seq_len, int per_seq_layers, FusedShape* f) {
   if (p.n_row_groups != 1 || p.groups > kFusedMaxItems) return false;
   const int G = (int)p.groups;
   const int gb = (max_seq_len + kBlock - 1) / kBlock;
@@ -2445,17 +2498,20 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
       cap = cap2;
       continue;
     }
-    // Every group gets the same number of items, even if some CUs stay idle: extra items
-    // would only shrink the items of some groups, while the largest items set the end of the
-    // call, and the workgroups left with them stream alone at the end.  Measured on 28 layers
-    // at 8K: 224 equal items 39.4 us against 256 mixed items (102 and 128 blocks) 41.2 us.
-    const int extra = 0;
-    const int grid = G * base + extra;
+    // Groups of one length (one sequence, or no per-sequence lengths) get the same number of
+    // items each, even if some CUs stay idle: extra items would only shrink the items of some
+    // groups, while the largest items set the end of the call, and the workgroups left with
+    // them stream alone at the end (28 layers at 8K: 224 equal items 39.4 us against 256 mixed
+    // items of 102 and 128 blocks 41.2 us).  A batch with per-sequence lengths launches every
+    // workgroup the device holds and the kernel gives each sequence items in proportion to its
+    // length, none over maxblk blocks (a config-4 layer, 32 sequences of 2K-32K tokens: the
+    // longest groups' 512-block items became about 340 blocks).
+    const int grid = per_seq_layers > 0 ? cap : G * base;
     if (grid > kFusedMaxItems || grid > part_cap) return false;
     f->gb = gb;
     f->base = base;
-    f->extra = extra;
-    f->maxblk = maxblk;  // groups with base+1 items have smaller items
+    f->layers = per_seq_layers;
+    f->maxblk = maxblk;
     f->grid = grid;
     f->ntg = ntg;
     f->lds = lds;
@@ -2467,10 +2523,11 @@ static bool fused_shape(const Plan& p, int R, int max_seq_len, FusedShape* f) {
 template <int D, int NT, int W>
 static bool try_fused_w(AttnArgs a, const Plan& p, hipStream_t st) {
   FusedShape f;
-  if (!fused_shape<D, NT, W>(p, a.R, a.max_seq_len, &f)) return false;
+  const int psl = (a.seq_lens && a.B > 1 && a.B <= kWave) ? (int)(p.groups / ((int64_t)a.B * a.KV)) : 0;
+  if (!fused_shape<D, NT, W>(p, a.R, a.max_seq_len, psl, &f)) return false;
   a.f_gb = f.gb;
   a.f_base = f.base;
-  a.f_extra = f.extra;
+  a.f_layers = f.layers;
   a.f_maxblk = f.maxblk;
   constexpr int NTGN = fused_ntg(D, W), NTGW = fused_ntg_wide(D, W, NT);
   if (f.ntg == NTGN)
@@ -2492,16 +2549,17 @@ static bool try_fused(AttnArgs a, const Plan& p, hipStream_t st) {
   return try_fused_w<D, NT, fused_waves<D, NT>()>(a, p, st);
 }
 
-// workgroups of the single-launch kernel for these sizes, or 0 (three-launch path)
+// workgroups of the single-launch kernel for these sizes, or 0 (another path); per_seq_layers
+// as for fused_shape (whether the single launch serves a shape does not depend on it)
 template <int D>
-static int fused_grid_for(const Plan& p, int R, int max_seq_len) {
+static int fused_grid_for(const Plan& p, int R, int max_seq_len, int per_seq_layers = 0) {
   FusedShape f;
   bool ok = false;
   switch (p.NT) {
-    case 1: ok = fused_shape<D, 1, fused_waves<D, 1>()>(p, R, max_seq_len, &f); break;
-    case 2: ok = fused_shape<D, 2, fused_waves<D, 2>()>(p, R, max_seq_len, &f); break;
-    case 3: ok = fused_shape<D, 3, fused_waves<D, 3>()>(p, R, max_seq_len, &f); break;
-    default: ok = fused_shape<D, 4, fused_waves<D, 4>()>(p, R, max_seq_len, &f); break;
+    case 1: ok = fused_shape<D, 1, fused_waves<D, 1>()>(p, R, max_seq_len, per_seq_layers, &f); break;
+    case 2: ok = fused_shape<D, 2, fused_waves<D, 2>()>(p, R, max_seq_len, per_seq_layers, &f); break;
+    case 3: ok = fused_shape<D, 3, fused_waves<D, 3>()>(p, R, max_seq_len, per_seq_layers, &f); break;
+    default: ok = fused_shape<D, 4, fused_waves<D, 4>()>(p, R, max_seq_len, per_seq_layers, &f); break;
   }
   return ok ? f.grid : 0;
 }
@@ -2643,7 +2701,7 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.stats = reinterpret_cast<float2*>(ws + p.off_stats);
   a.partial = reinterpret_cast<float*>(ws + p.off_partial);
   a.sync = reinterpret_cast<unsigned*>(ws);
-  a.f_gb = a.f_base = a.f_extra = a.f_maxblk = 0;  // chosen at launch
+  a.f_gb = a.f_base = a.f_layers = a.f_maxblk = 0;  // chosen at launch
   const int64_t D = head_dim, S = q_len, H = q_heads;
   a.q_sb = H * S * D;
   a.q_ls = (int64_t)batch * a.q_sb;
@@ -2877,5 +2935,6 @@ extern "C" int32_t sdv_attention_single_launch(int32_t num_layers, int32_t batch
   Plan p;
   if (!make_plan(num_layers, batch, q_heads, kv_heads, q_len, head_dim, max_seq_len, &p)) return 0;
   const int R = (q_heads / kv_heads) * q_len;
-  return head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len) : fused_grid_for<64>(p, R, max_seq_len);
+  const int psl = (batch > 1 && batch <= kWave) ? num_layers : 0;  // a batch is taken to pass its lengths
+  return head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len, psl) : fused_grid_for<64>(p, R, max_seq_len, psl);
 }

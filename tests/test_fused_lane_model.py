@@ -192,3 +192,114 @@ def test_planted_row_shift_direction_fails():
             written, _ = owner_stage(nvq, 6, right=True)
             for o, v in written.items():
                 assert v == sum(1000 * (cc + 1) + o for cc in range(nvq))
+
+
+# ---------------------------------------------------------------- per-sequence item plan
+def seq_plan(lens, L, KV, maxblk, grid, bisect=True):
+    """fused_kernel's item plan for a batch with per-sequence lengths: workgroup -> (group, c,
+    items of the group, blocks of the group, first item) or None past the plan, replayed with
+    the kernel's integer arithmetic: ceil(blocks / S) items per sequence (at most 32, at most one
+    per block, one for an empty sequence) for the smallest S in [1, maxblk] whose items fit the
+    grid.  bisect=False: a plain proportional share instead (a planted mistake)."""
+    B = len(lens)
+    blk = [-(-t // 16) for t in lens]
+    gs = L * KV
+
+    def items_for(sz):
+        return [1 if t == 0 else min(32, b, -(-b // sz)) for t, b in zip(lens, blk)]
+
+    if bisect:
+        lo, hi = 1, maxblk
+        while lo < hi:
+            mid = (lo + hi) // 2
+            if gs * sum(items_for(mid)) <= grid:
+                hi = mid
+            else:
+                lo = mid + 1
+        items = items_for(lo)
+    else:
+        total = gs * sum(blk)
+        items = [1 if t == 0 else min(32, b, 1 + ((grid - gs * B) * gs * b) // total) for t, b in zip(lens, blk)]
+    excl = [sum(items[:i]) for i in range(B)]
+    per_layer = KV * sum(items)
+    out = []
+    for item in range(grid):
+        li = item // per_layer
+        if li >= L:
+            out.append(None)
+            continue
+        r = item - li * per_layer
+        bs = next(b for b in range(B) if KV * excl[b] <= r < KV * (excl[b] + items[b]))
+        h, c = divmod(r - KV * excl[bs], items[bs])
+        out.append(((li * B + bs) * KV + h, c, items[bs], blk[bs], item - c))
+    return out
+
+
+def host_shape(max_len, G, cap):
+    """The host planner's items per group (base) and LDS width in blocks (maxblk)."""
+    gb = -(-max_len // 16)
+    base = min(32, gb, cap // G)
+    return base, -(-gb // base)
+
+
+def check_seq_plan(lens, L, KV, cap, bisect=True):
+    G = L * len(lens) * KV
+    base, maxblk = host_shape(max(lens), G, cap)
+    plan = seq_plan(lens, L, KV, maxblk, cap, bisect)
+    assert sum(e is not None for e in plan) <= cap
+    seen = {}
+    for item, e in enumerate(plan):
+        if e is None:
+            continue
+        grp, c, n_g, gbg, item0 = e
+        seen.setdefault(grp, []).append((c, item, n_g, gbg, item0))
+    assert sorted(seen) == list(range(G)), "every group has items"
+    for grp, its in seen.items():
+        its.sort()
+        n_g, gbg = its[0][2], its[0][3]
+        assert [c for c, *_ in its] == list(range(n_g)), "items of a group: c = 0 .. n_g-1"
+        assert [i for _, i, *_ in its] == list(range(its[0][4], its[0][4] + n_g)), "contiguous"
+        covered = 0
+        for c, *_ in its:
+            lo, hi = c * gbg // n_g, (c + 1) * gbg // n_g
+            assert lo == covered
+            covered = hi
+            assert hi - lo <= maxblk, f"item of {hi - lo} blocks over the LDS width {maxblk}"
+            assert gbg == 0 or hi - lo >= 1, "empty item in a non-empty sequence"
+        assert covered == gbg
+    return plan
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_per_sequence_item_plan(seed):
+    import random
+    rng = random.Random(seed)
+    B = rng.randint(2, 64)
+    L = rng.choice([1, 1, 2, 4])
+    KV = rng.choice([1, 2])
+    cap = rng.choice([224, 256, 512])
+    if L * B * KV > cap:
+        B = max(2, cap // (L * KV))
+    top = rng.choice([17, 2048, 8192, 32768])
+    lens = [rng.choice([0, 1, rng.randint(1, top), top]) for _ in range(B)]
+    if max(lens) == 0:
+        lens[0] = 5
+    check_seq_plan(lens, L, KV, cap)
+
+
+def test_per_sequence_plan_config4_layer():
+    """Config 4's per-layer call: the longest items shrink from 512 blocks."""
+    import random
+    rng = random.Random(41)
+    lens = [2048, 32768] + [rng.randint(2048, 32768) for _ in range(30)]
+    plan = check_seq_plan(lens, 1, 2, 256)
+    longest = max(-(-e[3] // e[2]) for e in plan if e is not None)
+    assert longest < 512
+
+
+def test_planted_plain_proportional_share_overflows_lds():
+    """A plain proportional share gives a sequence just short of a share threshold too few
+    items, and one of them overflows the LDS width."""
+    lens = [32768] * 31 + [30000]
+    with pytest.raises(AssertionError):
+        check_seq_plan(lens, 1, 2, 256, bisect=False)

@@ -146,9 +146,10 @@ int sdv_attention_workspace_status(const void* workspace, size_t workspace_bytes
  * Bound of every cross-workgroup wait of the single-launch path, in polls, for calls issued
  * after this one; 0 restores the default (2^20 polls; a poll waits for a device-scope load,
  * about a microsecond, so the default gives up after about a second).  A wait expires at its
- * `polls`-th unsuccessful poll: 1 gives up at the first entry not yet published.  For tests
- * of the failure path: a tiny bound makes waits expire while every workgroup still runs to
- * its end.  No counterpart in the reference.
+ * `polls`-th unsuccessful poll: 1 gives up at the first entry not yet published.
+ * UINT32_MAX makes every wait give up at its first check, whether or not the entries it waits
+ * for are published.  For tests of the failure path: waits expire while every workgroup still
+ * runs to its end.  No counterpart in the reference.
  */
 int sdv_attention_set_wait_limit(uint32_t polls);
 

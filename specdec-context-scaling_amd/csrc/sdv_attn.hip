@@ -1222,7 +1222,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
             bool ready = true;
 #pragma unroll
             for (int k = 0; k < PB; ++k) ready = ready && has_tag(em[k], a.tag) && has_tag(el[k], a.tag);
-            if (__ballot(!ready) == 0) break;
+            if (__ballot(!ready) == 0 && a.spin_limit != 0) break;  // 0: give up at once (tests)
             if (++spins >= a.spin_limit) {
               expired = true;
               break;
@@ -1653,7 +1653,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(AttnArgs a) {
       bool ready = true;
 #pragma unroll
       for (int r = 0; r < kOutLoads; ++r) ready = ready && v[r][0] != 0u && v[r][1] != 0u && v[r][2] != 0u && v[r][3] != 0u;
-      if (__ballot(!ready) == 0) break;
+      if (__ballot(!ready) == 0 && a.spin_limit != 0) break;  // 0: give up at once (tests)
       if (++spins >= a.spin_limit) {
         if (lane == 0) s_fail = 1;
         break;
@@ -2573,6 +2573,63 @@ static void launch_qk_pv(const AttnArgs& a, const Plan& p, int zdim, hipStream_t
     hipLaunchKernelGGL((pv_kernel<D, NT>), dim3(p.n_pv_chunks, gy, zdim), dim3(256), 0, st, a);
 }
 
+// Tag of a single-launch call: unique among the process's calls (never 0; 31 bits), with
+// kTagGraph set when the stream is recording a graph (whose replays reuse the tag).
+static std::atomic<uint32_t> g_calls{0};
+static std::atomic<uint32_t> g_wait_limit{0};  // 0: kDefaultSpinLimit
+
+static uint32_t next_call_tag(hipStream_t st) {
+  uint32_t t = 0;
+  while (t == 0) t = (g_calls.fetch_add(1, std::memory_order_relaxed) + 1u) & ~kTagGraph;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess)
+    (void)hipGetLastError();
+  else if (cs == hipStreamCaptureStatusActive)
+    t |= kTagGraph;
+  return t;
+}
+
+// polls per wait for the kernels: 0 (from UINT32_MAX) makes every wait give up at its first
+// check, published or not (tests of the failure path)
+static uint32_t wait_limit() {
+  const uint32_t v = g_wait_limit.load(std::memory_order_relaxed);
+  return v == 0xFFFFFFFFu ? 0u : v ? v : kDefaultSpinLimit;
+}
+
+// A multi-layer problem the single launch cannot hold at once, whose layers it can, with at least
+// this much work per layer (batch x KV heads x max_seq_len): one single launch per layer on the
+// same stream, each with its own call tag.  A config-4 call (28 layers x 32 sequences of 2K-32K
+// tokens) takes 28 x 85 us this way against 2.57 ms on the per-group kernel; with little work
+// per layer the per-group kernel's one launch wins (a one-layer call costs about 9 us).
+constexpr int64_t kPerLayerMinWork = 1 << 18;
+
+template <int D>
+static bool try_fused_per_layer(const AttnArgs& a, int layers, hipStream_t st) {
+  if (layers < 2 || (int64_t)a.B * a.KV * a.max_seq_len < kPerLayerMinWork) return false;
+  Plan pl;
+  if (!make_plan(1, a.B, a.G * a.KV, a.KV, a.S, D, a.max_seq_len, &pl) || pl.n_row_groups != 1 ||
+      fused_grid_for<D>(pl, a.R, a.max_seq_len) <= 0)
+    return false;
+  for (int l = 0; l < layers; ++l) {
+    AttnArgs al = a;
+    al.q = a.q + l * a.q_ls;
+    al.out = a.out + l * a.q_ls;
+    al.k_pages = a.k_pages + l * a.k_ls;
+    al.v_pages = a.v_pages + l * a.v_ls;
+    al.v_scales = a.v_scales + l * a.s_ls;
+    al.k_ls = al.v_ls = al.s_ls = 0;
+    al.q_ls = 0;
+    if (l > 0) al.tag = next_call_tag(st);
+    switch (pl.NT) {
+      case 1: try_fused<D, 1>(al, pl, st); break;
+      case 2: try_fused<D, 2>(al, pl, st); break;
+      case 3: try_fused<D, 3>(al, pl, st); break;
+      default: try_fused<D, 4>(al, pl, st); break;
+    }
+  }
+  return true;
+}
+
 template <int D>
 static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
   if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
@@ -2591,6 +2648,7 @@ static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t s
       default: done = try_fused<D, 4>(a, p, st); break;
     }
     if (done) return;
+    if (!a.app_v && try_fused_per_layer<D>(a, zdim / a.B, st)) return;
     if (p.group) {  // many one-tile groups: persistent workgroups, whole groups each
       hipLaunchKernelGGL(group_kernel<D>, dim3(kGroupGrid), dim3(64 * kGroupWaves), 0, st, a, (int)p.groups,
                          zdim / a.B, p.tpad);
@@ -2618,27 +2676,6 @@ extern "C" size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch
   Plan p;
   if (!make_plan(num_layers, batch, q_heads, kv_heads, q_len, head_dim, max_seq_len, &p)) return 0;
   return p.total;
-}
-
-// Tag of a single-launch call: unique among the process's calls (never 0; 31 bits), with
-// kTagGraph set when the stream is recording a graph (whose replays reuse the tag).
-static std::atomic<uint32_t> g_calls{0};
-static std::atomic<uint32_t> g_wait_limit{0};  // 0: kDefaultSpinLimit
-
-static uint32_t next_call_tag(hipStream_t st) {
-  uint32_t t = 0;
-  while (t == 0) t = (g_calls.fetch_add(1, std::memory_order_relaxed) + 1u) & ~kTagGraph;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess)
-    (void)hipGetLastError();
-  else if (cs == hipStreamCaptureStatusActive)
-    t |= kTagGraph;
-  return t;
-}
-
-static uint32_t wait_limit() {
-  const uint32_t v = g_wait_limit.load(std::memory_order_relaxed);
-  return v ? v : kDefaultSpinLimit;
 }
 
 // The new tokens to append before attending (sdv_paged_attention_append).

@@ -129,7 +129,7 @@ def test_token_major_q_layout(cuda_device):
 @pytest.mark.parametrize("split", [False, True])
 def test_config4_batch32_ragged(cuda_device, split):
     """B=32, T_b ~ U{2048..32768}, fragmented pool: every sequence within the bar, through the
-    single launch (items of up to 512 blocks) and through the three launches one at a time."""
+    single launch (items sized per sequence) and through the three launches one at a time."""
     announce(f"attn config4 B=32 ragged split={split}")
     lens = wl.ragged_lengths(32, 2048, 32768, seed=4)
     got, want = _run_case(cuda_device, 12, 2, 128, lens, 1, seed=73, split=split)
@@ -372,12 +372,16 @@ def test_verify_wide_split(cuda_device, layers, h, d, lens):
 
 def test_multi_layer_batch32_ragged(cuda_device):
     """Config 4: B=32 contexts U{2048..32768}, fragmented pool, 1% outlier V channels x20,
-    28 layers in one launch; the shortest, the longest and the first sequence are checked."""
+    28 layers in one call, which runs one single launch per layer (the whole call has more
+    groups than the device holds at once, one layer does not); the shortest, the longest and
+    the first sequence are checked on the first, a middle and the last layer."""
     lens = wl.ragged_lengths(32, 2048, 32768, seed=41)
     announce(f"attn multi-layer B=32 ragged 28x12/2/128 T={min(lens)}..{max(lens)}")
+    assert ops.single_launch_workgroups(28, 32, 12, 2, 1, 128, max(lens)) == 0
+    assert ops.single_launch_workgroups(1, 32, 12, 2, 1, 128, max(lens)) > 0
     cache = _filled_cache(cuda_device, 28, 2, 128, lens, seed=520, outliers=True)
     seqs = sorted({0, lens.index(min(lens)), lens.index(max(lens))})
-    _check_multi_layer(cuda_device, cache, 12, 1, (0, 27), seqs, "B=32 ragged", seed=521)
+    _check_multi_layer(cuda_device, cache, 12, 1, (0, 13, 27), seqs, "B=32 ragged", seed=521)
     fp = cache.footprint()
     assert fp["tokens"] == sum(lens)
     assert abs(fp["saved_frac"] - (1 - 776 / 1024)) < 1e-9

@@ -1,9 +1,9 @@
 """The single launch's failure path on the GPU, driven from the host.
 
-The single launch's cross-workgroup waits are bounded (csrc/sdv_attn.hip, fused_kernel).  A
-host-set bound of one poll (sdv_attention_set_wait_limit) makes them give up at the first
-entry not yet published, while every workgroup still runs to its end -- no kernel is made to
-fault or hang.  Checked: the failure is surfaced (NaN outputs where the call could not
+The single launch's cross-workgroup waits are bounded (csrc/sdv_attn.hip, fused_kernel).  The
+host sets the bound that makes every wait give up at its first check (sdv_attention_set_wait_limit
+with UINT32_MAX; a bound of one poll gives up only at an entry not yet published, which depends
+on timing), while every workgroup still runs to its end -- no kernel is made to fault or hang.  Checked: the failure is surfaced (NaN outputs where the call could not
 complete, the workspace's failure count), outputs that did complete are exact, the next eager
 call on the same workspace is exact, and a graph-recorded call that failed poisons the
 workspace so that later graph replays are refused (NaN, counted) until the workspace is
@@ -26,6 +26,7 @@ from specdec_amd.kernels import ops
 pytestmark = pytest.mark.gpu
 
 L, KV, H, D, T = 28, 2, 12, 128, 2048
+GIVE_UP = 0xFFFFFFFF  # wait bound: every wait gives up at its first check
 
 
 def _cache(dev):
@@ -69,19 +70,19 @@ def restore_wait_limit():
 
 
 def test_expired_waits_are_surfaced_and_the_next_call_is_exact(cuda_device, restore_wait_limit):
-    announce("sync failure: eager call with a one-poll wait bound, then a normal call")
+    announce("sync failure: eager call whose waits give up, then a normal call")
     assert ops.single_launch_workgroups(L, 1, H, KV, 1, D, T) > 0
     cache = _cache(cuda_device)
     g = wl.gen(882, cuda_device)
     q = torch.randn((L, 1, H, 1, D), generator=g, device=cuda_device).to(torch.bfloat16)
     ws = ops.new_workspace(cuda_device, ops.attention_workspace_bytes(L, 1, H, KV, 1, D, T))
     out = torch.empty_like(q)
-    ops.set_wait_limit(1)
+    ops.set_wait_limit(GIVE_UP)
     _call(cache, q, ws, out)
     torch.cuda.synchronize()
     fails, poisoned = ops.workspace_status(ws)
     nans = _check_partial(out, cache, q)
-    print(f"one-poll bound: {fails} failures, {nans} NaN outputs of {out.numel()}")
+    print(f"waits given up: {fails} failures, {nans} NaN outputs of {out.numel()}")
     assert fails > 0 and nans > 0, "expired waits were not surfaced"
     assert not poisoned, "an eager call must not poison the workspace"
     with pytest.raises(ops.SdvError):
@@ -101,7 +102,7 @@ def test_expired_waits_are_surfaced_and_the_next_call_is_exact(cuda_device, rest
 
 
 def test_graph_poison_refuses_replays_until_reset(cuda_device, restore_wait_limit):
-    announce("sync failure: graph-recorded call with a one-poll wait bound, poison, reset")
+    announce("sync failure: graph-recorded call whose waits give up, poison, reset")
     cache = _cache(cuda_device)
     g = wl.gen(883, cuda_device)
     q = torch.randn((L, 1, H, 1, D), generator=g, device=cuda_device).to(torch.bfloat16)
@@ -126,7 +127,7 @@ def test_graph_poison_refuses_replays_until_reset(cuda_device, restore_wait_limi
             assert_close(out[layer].cpu(), _want(cache, q, layer), f"replay layer {layer}")
     assert ops.workspace_status(ws) == (0, False)
 
-    ops.set_wait_limit(1)
+    ops.set_wait_limit(GIVE_UP)
     bad = torch.cuda.CUDAGraph()
     with torch.cuda.graph(bad):
         step()
@@ -134,7 +135,7 @@ def test_graph_poison_refuses_replays_until_reset(cuda_device, restore_wait_limi
     bad.replay()
     torch.cuda.synchronize()
     fails, poisoned = ops.workspace_status(ws)
-    print(f"graph replay with a one-poll bound: {fails} failures, poisoned={poisoned}")
+    print(f"graph replay whose waits give up: {fails} failures, poisoned={poisoned}")
     assert fails > 0 and poisoned
 
     good.replay()                # refused: every output NaN, counted

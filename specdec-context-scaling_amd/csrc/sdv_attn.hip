@@ -1831,13 +1831,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   const int blo = min(nblk_wg, split * part);
   const int bhi = min(nblk_wg, blo + part);
 
-  float m_run[NT], l_run[NT], c_run[NT];   // pass 1: running max, sum and the sum's compensation
+  float m_run[NT], l_run[NT];   // pass 1: running max and sum
   float nml[NT], invl[NT];      // pass 2: -M log2 e and 1/L per row
   f32x4 acc[DT][NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     m_run[nt] = -INFINITY;
-    l_run[nt] = c_run[nt] = 0.0f;
+    l_run[nt] = 0.0f;
     nml[nt] = 0.0f;
     invl[nt] = 0.0f;
     if (OUT && rv[nt]) {
@@ -1895,6 +1895,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       const int jg0 = w0 + 2 * s2;  // global block of u = 0
       bf16x8 pop[NT];
       uint32_t pw[NT][4];           // packed BF16 probabilities: u = 0 in words 0-1, u = 1 in 2-3
+      float sv[NT][8];              // pass 1: the stage's scores, u = 0 in 0-3, u = 1 in 4-7
       const bool mine = 2 * s2 < jn;  // wave-uniform: the stage has keys this wavefront's rows see
       // every key of the stage exists, is valid and is seen by every row: no mask
       const bool full = 2 * s2 + 1 < jn && x.pb[0] >= 0 && x.pb[1] >= 0 && (jg0 + 2) * kBlock - 1 <= kmin;
@@ -1903,7 +1904,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
         const bool have = 2 * s2 + u < jn;  // wave-uniform
         if (!have) {
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) pw[nt][2 * u] = pw[nt][2 * u + 1] = 0u;
+          for (int nt = 0; nt < NT; ++nt) {
+            pw[nt][2 * u] = pw[nt][2 * u + 1] = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[nt][4 * u + i] = -INFINITY;
+          }
           continue;
         }
         const int t0 = (jg0 + u) * kBlock + 4 * g;
@@ -1922,32 +1927,38 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
             s4[i] = (full || (blk_ok && t0 + i <= lim[nt])) ? v : -INFINITY;
           }
           if constexpr (!OUT) {
-            // Online (max, sum) over the whole context in one lane: the sum is rescaled by
-            // exp2((m_old - m_new) log2 e), which is exactly 1 while the max stays (the one-FMA
-            // form exp2(m_old log2 e - RN(m_new log2 e)) is off by the product's rounding on every
-            // block, and L drifted by ~1e-5 at T = 8192: rel-L2 7e-4 against eager), and the
-            // sum is compensated (T/4 terms go into one fp32 accumulator; the compensation is
-            // rescaled with it).
-            const float mt = fmaxf(fmaxf(s4[0], s4[1]), fmaxf(s4[2], s4[3]));
-            if (mt != -INFINITY) {
-#pragma clang fp contract(off)
-              const float mn = fmaxf(m_run[nt], mt), nm = -mn * kLog2e;
-              const float f = (m_run[nt] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
-              float e[4];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nm));
-              const float x = (e[0] + e[1]) + (e[2] + e[3]);
-              const float l = l_run[nt] * f, t = l + x;
-              c_run[nt] = c_run[nt] * f + ((l >= x) ? ((l - t) + x) : ((x - t) + l));
-              l_run[nt] = t;
-              m_run[nt] = mn;
-            }
+            for (int i = 0; i < 4; ++i) sv[nt][4 * u + i] = s4[i];
           } else {
             float p[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml[nt])) * invl[nt];
             pw[nt][2 * u] = pack_bf16x2(p[0], p[1]);
             pw[nt][2 * u + 1] = pack_bf16x2(p[2], p[3]);
+          }
+        }
+      }
+      if constexpr (!OUT) {
+        // Online (max, sum) per lane, one update per stage: the max of the stage's eight scores
+        // first, then the running sum rescaled once by exp2((m_old - m_new) log2 e), which is
+        // exactly 1 while the max stays (the one-FMA form exp2(m_old log2 e - RN(m_new log2 e))
+        // is off by the product's rounding on every update, and L drifted by ~1e-5 at T = 8192:
+        // rel-L2 7e-4 against eager).  A lane sums at most T/32 terms of at most 1 each, so the
+        // plain fp32 sum is within ~1e-5 relative of the exact one.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float mt = fmaxf(fmaxf(fmaxf(sv[nt][0], sv[nt][1]), fmaxf(sv[nt][2], sv[nt][3])),
+                                 fmaxf(fmaxf(sv[nt][4], sv[nt][5]), fmaxf(sv[nt][6], sv[nt][7])));
+          if (mt != -INFINITY) {
+#pragma clang fp contract(off)
+            const float mn = fmaxf(m_run[nt], mt), nm = -mn * kLog2e;
+            const float f = (m_run[nt] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
+            float e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[nt][i], kLog2e, nm));
+            const float x = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+            l_run[nt] = l_run[nt] * f + x;
+            m_run[nt] = mn;
           }
         }
       }
@@ -2021,7 +2032,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     // (max, sum) of each row over the four lane groups, in a fixed order
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      float m = m_run[nt], l = l_run[nt] + c_run[nt];
+      float m = m_run[nt], l = l_run[nt];
       merge_lanes<16>(m, l);
       merge_lanes<32>(m, l);
       if (g == 0 && rv[nt]) st[(int64_t)(row0 + nt * 16 + n) * kPrefillSplit + split] = make_float2(m, l);

@@ -1750,8 +1750,7 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // of each stage through LDS (per wavefront it would cost twice the conversions: 588-604 us).
 constexpr int kPrefillRows = 16;   // query rows per wavefront (16 per MFMA row tile)
 constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
-// stages (two blocks each) in flight per wavefront: 3 measured equal, 4 slower (fewer resident
-// wavefronts in pass 2)
+// pass 1: stages (two blocks each) in flight per wavefront (3 measured equal, 4 slower)
 constexpr int kPrefillRing = 2;
 // Pass 1 splits each row group's keys in 8 parts, one workgroup each (eight times the
 // wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1 with one
@@ -1858,6 +1857,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   // A stage is two consecutive blocks u = 0, 1: K operands, page ids and, for pass 2, the V
   // words of this wavefront's dimension tiles wave*DTW .. (lane (g, n): dimension dt*16 + n,
   // tokens 4g..4g+3) and the four scales of those tokens.
+  // Pass 2 keeps one stage in registers and issues the next stage's loads inside the stage,
+  // once its registers are dead (106 VGPRs + 36 AGPRs for head_dim 128: three wavefronts per
+  // SIMD, two with two stages; 82 + 20 for head_dim 64).  2048 x 8192, pass 2: 298-301 ->
+  // 290-295 us (12/2/128), 217-220 -> 211-213 us (14/2/64, where two stages loaded after the
+  // stage's products measured 217-220 and one 220-226 us).
+  constexpr int RING = OUT ? 1 : kPrefillRing;
   struct Stage {
     bf16x8 k[2][KK];
     uint32_t v[2][OUT ? DTW : 1];
@@ -1993,9 +1998,19 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
               make_uint4(pack_bf16x2(f01.x * x.sc[0].x, f01.y * x.sc[0].y), pack_bf16x2(f23.x * x.sc[0].z, f23.y * x.sc[0].w),
                          pack_bf16x2(f45.x * x.sc[1].x, f45.y * x.sc[1].y), pack_bf16x2(f67.x * x.sc[1].z, f67.y * x.sc[1].w));
         }
+        if constexpr (RING == 1) {
+          // The stage's registers are dead now (K multiplied, V codes and scales in LDS): the
+          // next stage's loads go out here, and the barrier waits for LDS only, so they stay in
+          // flight under it and under this stage's p.V products.
+          load_stage(s2 + 1, x);
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+          __builtin_amdgcn_s_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        } else {
+          __syncthreads();
+        }
         // every wavefront's tiles are in LDS; the other buffer is free again (its readers passed
         // this barrier after their own reads of the previous stage)
-        __syncthreads();
         if (mine) {
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
@@ -2012,9 +2027,6 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     // workgroup's window in every wavefront (each dequantizes its share of the V operand, with
     // a barrier per stage); pass 1 only this wavefront's blocks.
     const int nst = OUT ? ((wn + 1) >> 1) : ((jn + 1) >> 1);
-    // pass 2 for head_dim 128 keeps one stage: 98 VGPRs + 36 AGPRs, three wavefronts per SIMD
-    // (two with two stages), which the two key parts fill
-    constexpr int RING = (OUT && D == 128) ? 1 : kPrefillRing;
     Stage ring[RING];
 #pragma unroll
     for (int i = 0; i < RING; ++i) load_stage(i, ring[i]);
@@ -2023,7 +2035,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       for (int i = 0; i < RING; ++i) {
         const int ss = s2 + i;
         if (ss < nst) compute_stage(ss, ring[i]);  // workgroup-uniform in pass 2, wave-uniform in pass 1
-        load_stage(ss + RING, ring[i]);
+        if (!OUT || RING > 1 || ss >= nst) load_stage(ss + RING, ring[i]);  // else done inside
       }
     }
   }

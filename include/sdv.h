@@ -128,6 +128,11 @@ size_t sdv_attention_workspace_size(int32_t num_layers, int32_t batch, int32_t q
  * every graph-recorded call writes NaN to all of its outputs and counts itself instead of
  * running, until sdv_attention_workspace_init clears the area.  Eager calls take a fresh tag
  * each and are unaffected.
+ *
+ * A NULL workspace names the current device's no-allocation scratch (the workspace of
+ * sdv_paged_attention_noalloc; workspace_bytes is then ignored): this clears its failure
+ * count and graph poison.  The first use of the scratch on a device must not be recorded into
+ * a graph (SDV_ERR_UNSUPPORTED), as for sdv_paged_attention_noalloc.
  */
 #define SDV_SYNC_BYTES 12583168
 int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
@@ -136,8 +141,10 @@ int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* 
  * Read words 0 and 1 of a workspace's synchronisation area: `failures` = expired waits and
  * refused calls of the single-launch path since the last sdv_attention_workspace_init, and
  * `poisoned` != 0 when graph-recorded calls are refused (see above).  Synchronises `stream`
- * (a device-to-host copy); not for use while a graph is being recorded.  No counterpart in
- * the reference.
+ * (a device-to-host copy); not for use while a graph is being recorded.  A NULL workspace
+ * names the current device's no-allocation scratch (workspace_bytes ignored), whose words
+ * count the failed and refused calls of sdv_paged_attention_noalloc.  No counterpart in the
+ * reference.
  */
 int sdv_attention_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* failures,
                                    uint32_t* poisoned, void* stream);
@@ -253,9 +260,12 @@ int sdv_paged_attention_append(const void* q, const void* k_pages, const void* v
  * sdv_paged_attention without a workspace argument and without allocating: the library's own
  * device-resident scratch array (one per GPU, SDV_NOALLOC_MAX_WORKSPACE bytes, held until the
  * process ends) serves as the workspace.  Arguments and results as sdv_paged_attention.  Calls
- * whose chosen path needs more than the array holds return SDV_ERR_WORKSPACE (the single
- * launch -- decode and verify shapes that fit the device at once -- needs SDV_SYNC_BYTES;
- * the three-launch path needs sdv_attention_workspace_size bytes).  Every call on one GPU
+ * whose chosen path needs more than the array holds return SDV_ERR_WORKSPACE before launching
+ * anything (the single launch -- decode and verify shapes that fit the device at once, also
+ * when a multi-layer call runs it once per layer -- needs SDV_SYNC_BYTES; the per-group
+ * kernel, the three-launch path and prefill rows need sdv_attention_workspace_size bytes).
+ * Expired waits and graph poison are counted in the scratch: read and clear them with
+ * sdv_attention_workspace_status / sdv_attention_workspace_init and a NULL workspace.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams, other threads) race,
  * so order them on one stream.  The first call on a device takes the array's address and
  * zeroes its synchronisation area, waiting for that to finish, so it must not be recorded

@@ -2575,13 +2575,19 @@ static bool try_fused(AttnArgs a, const Plan& p, hipStream_t st) {
 }
 
 // workgroups of the single-launch kernel for these sizes, or 0 (another path); per_seq_layers
-// as for fused_shape (whether the single launch serves a shape does not depend on it)
+// as for fused_shape (whether the single launch serves a shape does not depend on it).
+// append: the call writes new tokens in the kernel, which try_fused launches with the
+// wavefront count of an appending call (more LDS for one row tile, so a shape may fit without
+// the append and not with it): the answer is the one try_fused will act on.
 template <int D>
-static int fused_grid_for(const Plan& p, int R, int max_seq_len, int per_seq_layers = 0) {
+static int fused_grid_for(const Plan& p, int R, int max_seq_len, int per_seq_layers = 0, bool append = false) {
   FusedShape f;
   bool ok = false;
   switch (p.NT) {
-    case 1: ok = fused_shape<D, 1, fused_waves<D, 1>()>(p, R, max_seq_len, per_seq_layers, &f); break;
+    case 1:
+      ok = append ? fused_shape<D, 1, 16>(p, R, max_seq_len, per_seq_layers, &f)
+                  : fused_shape<D, 1, fused_waves<D, 1>()>(p, R, max_seq_len, per_seq_layers, &f);
+      break;
     case 2: ok = fused_shape<D, 2, fused_waves<D, 2>()>(p, R, max_seq_len, per_seq_layers, &f); break;
     case 3: ok = fused_shape<D, 3, fused_waves<D, 3>()>(p, R, max_seq_len, per_seq_layers, &f); break;
     default: ok = fused_shape<D, 4, fused_waves<D, 4>()>(p, R, max_seq_len, per_seq_layers, &f); break;
@@ -2655,14 +2661,18 @@ static bool try_fused_per_layer(const AttnArgs& a, int layers, hipStream_t st) {
   return true;
 }
 
+// Launches the call's kernels.  Only the single launch writes new tokens itself: a call with
+// a.app_v set that the single launch does not take returns false before anything is launched,
+// and the caller appends with the append kernel and calls again without a.app_v.
 template <int D>
-static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
+static bool launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
   if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
+    if (a.app_v) return false;
     const dim3 grid((unsigned)((a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves)), a.KV, zdim);
     const dim3 grid1(grid.x * kPrefillSplit, grid.y, grid.z), grid2(grid.x * a.pf_parts, grid.y, grid.z);
     if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPrefillWaves), 0, st, a);
     if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid2, dim3(64 * kPrefillWaves), 0, st, a);
-    return;
+    return true;
   }
   if (phases == SDV_PHASE_ALL) {
     bool done = false;
@@ -2672,14 +2682,16 @@ static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t s
       case 3: done = try_fused<D, 3>(a, p, st); break;
       default: done = try_fused<D, 4>(a, p, st); break;
     }
-    if (done) return;
-    if (!a.app_v && try_fused_per_layer<D>(a, zdim / a.B, st)) return;
+    if (done) return true;
+    if (a.app_v) return false;
+    if (try_fused_per_layer<D>(a, zdim / a.B, st)) return true;
     if (p.group) {  // many one-tile groups: persistent workgroups, whole groups each
       hipLaunchKernelGGL(group_kernel<D>, dim3(kGroupGrid), dim3(64 * kGroupWaves), 0, st, a, (int)p.groups,
                          zdim / a.B, p.tpad);
-      return;
+      return true;
     }
   }
+  if (a.app_v) return false;
   switch (p.NT) {
     case 1: launch_qk_pv<D, 1>(a, p, zdim, st, phases); break;
     case 2: launch_qk_pv<D, 2>(a, p, zdim, st, phases); break;
@@ -2688,6 +2700,26 @@ static void launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t s
   }
   if (phases & SDV_PHASE_REDUCE)
     hipLaunchKernelGGL(reduce_kernel<D>, dim3((a.R * D + 63) / 64, a.KV, zdim), dim3(256), 0, st, a);
+  return true;
+}
+
+// Workspace bytes the path launch_all takes for a call touches: the synchronisation area for
+// the single launch (also one per layer), the full layout otherwise (per-group kernel, three
+// launches, prefill rows).  The same decisions as launch_all and try_fused_per_layer.
+template <int D>
+static size_t path_workspace(const Plan& p, const AttnArgs& a, int layers, bool append) {
+  if (p.n_row_groups > 1) return p.total;
+  const int psl = (a.seq_lens && a.B > 1 && a.B <= kWave) ? layers : 0;
+  if (fused_grid_for<D>(p, a.R, a.max_seq_len, psl, append) > 0) return kSyncBytes;
+  // otherwise the append kernel runs first and the call takes the path of a call without it
+  if (append && fused_grid_for<D>(p, a.R, a.max_seq_len, psl) > 0) return kSyncBytes;
+  if (layers >= 2 && (int64_t)a.B * a.KV * a.max_seq_len >= kPerLayerMinWork) {
+    Plan pl;
+    if (make_plan(1, a.B, a.G * a.KV, a.KV, a.S, D, a.max_seq_len, &pl) && pl.n_row_groups == 1 &&
+        fused_grid_for<D>(pl, a.R, a.max_seq_len) > 0)
+      return kSyncBytes;
+  }
+  return p.total;
 }
 
 }  // namespace sdv
@@ -2732,15 +2764,7 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   const int64_t s_page = (int64_t)num_blocks * kv_heads * kBlock;
   if (num_layers > 1 && (k_layer_stride < k_page || v_layer_stride < k_page || s_layer_stride < s_page))
     return SDV_ERR_SHAPE;
-  // path_sized_ws: the workspace only has to hold what the chosen path touches (the
-  // synchronisation area for the single launch); otherwise sdv_attention_workspace_size bytes
-  size_t need = p.total;
-  if (path_sized_ws && phase_mask == SDV_PHASE_ALL) {
-    const int R = (q_heads / kv_heads) * q_len;
-    const int grid = head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len) : fused_grid_for<64>(p, R, max_seq_len);
-    if (grid > 0) need = kSyncBytes;
-  }
-  if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return SDV_ERR_WORKSPACE;
+  if (!workspace || !aligned(workspace, 256)) return SDV_ERR_WORKSPACE;
   if (!aligned(q, 16) || !aligned(out, 16) || !aligned(k_pages, 16) || !aligned(v_scales, 16) ||
       !aligned(v_pages, 4) || !aligned(block_table, 4) || !aligned(seq_lens, 4))
     return SDV_ERR_ALIGN;
@@ -2800,6 +2824,14 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.app_ls = 0;
   a.app_scale_mode = 0;
 
+  // path_sized_ws: the workspace only has to hold what the chosen path touches (the
+  // synchronisation area for the single launch); otherwise sdv_attention_workspace_size bytes
+  size_t need = p.total;
+  if (path_sized_ws && phase_mask == SDV_PHASE_ALL)
+    need = head_dim == 128 ? path_workspace<128>(p, a, num_layers, app != nullptr)
+                           : path_workspace<64>(p, a, num_layers, app != nullptr);
+  if (workspace_bytes < need) return SDV_ERR_WORKSPACE;
+
   hipStream_t st = static_cast<hipStream_t>(stream);
   a.tag = next_call_tag(st);
   a.spin_limit = wait_limit();
@@ -2811,15 +2843,21 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
     if (!aligned(app->k_new, 16) || !aligned(app->v_new, 16) || !aligned(app->slot_mapping, 4) ||
         (num_layers > 1 && app->layer_stride % 8 != 0))
       return SDV_ERR_ALIGN;
-    const int R = (q_heads / kv_heads) * q_len;
-    const bool fused = (head_dim == 128 ? fused_grid_for<128>(p, R, max_seq_len) : fused_grid_for<64>(p, R, max_seq_len)) > 0;
-    if (fused) {  // the single launch writes the new tokens itself
-      a.app_k = static_cast<const uint16_t*>(app->k_new);
-      a.app_v = static_cast<const uint16_t*>(app->v_new);
-      a.app_slots = app->slot_mapping;
-      a.app_ls = num_layers > 1 ? app->layer_stride : 0;
-      a.app_scale_mode = app->scale_mode;
-    } else if (app->slot_mapping) {  // other paths: the append kernel first, on the same stream
+    // offered to the single launch, which writes the new tokens itself; launch_all declines
+    // (launching nothing) when another path serves the call
+    a.app_k = static_cast<const uint16_t*>(app->k_new);
+    a.app_v = static_cast<const uint16_t*>(app->v_new);
+    a.app_slots = app->slot_mapping;
+    a.app_ls = num_layers > 1 ? app->layer_stride : 0;
+    a.app_scale_mode = app->scale_mode;
+  }
+  const int zdim = num_layers * batch;
+  auto launch = [&]() {
+    return head_dim == 128 ? launch_all<128>(a, p, zdim, st, phase_mask) : launch_all<64>(a, p, zdim, st, phase_mask);
+  };
+  if (!launch()) {
+    // other paths: the append kernel first, on the same stream, then the call without the append
+    if (app->slot_mapping) {
       const int st_app = sdv_quant_append(app->v_new, app->k_new, app->slot_mapping, batch * q_len, kv_heads,
                                           head_dim, head_dim, num_layers, app->layer_stride,
                                           const_cast<void*>(k_pages), const_cast<void*>(v_pages),
@@ -2834,12 +2872,10 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
                                             k_layer_stride, v_layer_stride, s_layer_stride, app->scale_mode, stream);
       if (st_app != SDV_OK) return st_app;
     }
+    a.app_k = a.app_v = nullptr;
+    a.app_slots = nullptr;
+    if (!launch()) return SDV_ERR_HIP;  // unreachable: without a.app_v every path launches
   }
-  const int zdim = num_layers * batch;
-  if (head_dim == 128)
-    launch_all<128>(a, p, zdim, st, phase_mask);
-  else
-    launch_all<64>(a, p, zdim, st, phase_mask);
   return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
 }
 
@@ -2888,13 +2924,6 @@ extern "C" int sdv_paged_attention(const void* q, const void* k_pages, const voi
                                     workspace_bytes, out, stream, SDV_PHASE_ALL);
 }
 
-extern "C" int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
-  if (!workspace) return SDV_ERR_NULL;
-  if (!aligned(workspace, 256) || workspace_bytes < kSyncBytes) return SDV_ERR_WORKSPACE;
-  hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<uint32_t*>(workspace), kSyncBytes / 4);
-  return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
-}
 
 // ---------------------------------------------------------------------------- no-allocation entry point
 // Device-resident workspace for sdv_paged_attention_noalloc: one copy per GPU the library runs
@@ -2958,13 +2987,35 @@ extern "C" int sdv_paged_attention_noalloc(const void* q, const void* k_pages, c
                    /*path_sized_ws=*/true);
 }
 
+// A NULL workspace in sdv_attention_workspace_init / _status names the current device's
+// no-allocation scratch (the workspace of sdv_paged_attention_noalloc), so its failure count
+// and graph poison can be read and cleared like a caller's workspace.
+static int resolve_workspace(void*& workspace, size_t& workspace_bytes, hipStream_t st) {
+  if (workspace) return SDV_OK;
+  const int rc = scratch_for_device(st, &workspace);
+  workspace_bytes = kScratchBytes;
+  return rc;
+}
+
+extern "C" int sdv_attention_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rc = resolve_workspace(workspace, workspace_bytes, st);
+  if (rc != SDV_OK) return rc;
+  if (!aligned(workspace, 256) || workspace_bytes < kSyncBytes) return SDV_ERR_WORKSPACE;
+  hipLaunchKernelGGL(zero_kernel, dim3(256), dim3(256), 0, st, static_cast<uint32_t*>(workspace), kSyncBytes / 4);
+  return hipGetLastError() == hipSuccess ? SDV_OK : SDV_ERR_HIP;
+}
+
 extern "C" int sdv_attention_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* failures,
                                               uint32_t* poisoned, void* stream) {
-  if (!workspace || !failures || !poisoned) return SDV_ERR_NULL;
-  if (!aligned(workspace, 256) || workspace_bytes < kSyncBytes) return SDV_ERR_WORKSPACE;
-  uint32_t head[2] = {0, 0};
+  if (!failures || !poisoned) return SDV_ERR_NULL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (hipMemcpyAsync(head, workspace, sizeof(head), hipMemcpyDeviceToHost, st) != hipSuccess ||
+  void* ws = const_cast<void*>(workspace);
+  const int rc = resolve_workspace(ws, workspace_bytes, st);
+  if (rc != SDV_OK) return rc;
+  if (!aligned(ws, 256) || workspace_bytes < kSyncBytes) return SDV_ERR_WORKSPACE;
+  uint32_t head[2] = {0, 0};
+  if (hipMemcpyAsync(head, ws, sizeof(head), hipMemcpyDeviceToHost, st) != hipSuccess ||
       hipStreamSynchronize(st) != hipSuccess) {
     (void)hipGetLastError();
     return SDV_ERR_HIP;

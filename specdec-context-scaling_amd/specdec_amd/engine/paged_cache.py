@@ -99,7 +99,10 @@ class PagedKVCache:
         self._bt = None
         self._tiles = None  # (lengths, device tile table) of the last prefill
         self._ws = None     # attention workspace owned by the pool
-        self._retired = []  # replaced workspaces, kept alive for graphs that recorded them
+        # replaced workspaces, kept alive for graphs that recorded them; each replacement is at
+        # least twice the size of the one before, so they hold at most the current one's bytes
+        self._retired = []
+        self._q_heads, self._q_len = 0, 0  # the largest query shape append_attend has served
 
     # ------------------------------------------------------------------ storage
     def _new_pages(self, nb: int):
@@ -138,21 +141,32 @@ class PagedKVCache:
         self.blocks[seq].extend(self.alloc.alloc(need))
         self._bt = None
 
-    def reserve_all(self, n_tokens: int) -> None:
-        """Blocks for the first n_tokens positions of every sequence, and the device block table
-        (before recording a graph that appends up to n_tokens)."""
+    def reserve_all(self, n_tokens: int, q_heads: int | None = None, q_len: int | None = None) -> None:
+        """Everything a recorded step up to n_tokens positions needs, before recording it: page
+        blocks for the first n_tokens positions of every sequence, the device block table, and
+        the attention workspace append_attend needs at that length for q_heads query heads and
+        q_len new tokens per call (default: the largest append_attend has served; with no call
+        served and none given, the workspace is sized by the first call)."""
         for b in range(self.batch):
             self.reserve(b, n_tokens)
         self.block_table()
+        heads = q_heads or self._q_heads
+        rows = max(q_len or 0, self._q_len, 1)
+        if heads:
+            tmax = max(n_tokens, max(self.lengths))
+            self.workspace(ops.attention_workspace_bytes(1, self.batch, heads, self.kv_heads, rows, self.head_dim,
+                                                         tmax))
 
     def workspace(self, nbytes: int) -> torch.Tensor:
-        """The pool's attention workspace, at least nbytes (a larger one replaces it; the old one is
-        kept alive, since a recorded graph may use it)."""
+        """The pool's attention workspace, at least nbytes.  A larger one (at least twice the
+        size) replaces it; the old one is kept alive, since a recorded graph may use it."""
         if self._ws is None or self._ws.numel() < nbytes:
             _no_recording(self.device, f"the attention workspace would grow to {nbytes} bytes")
+            grow = 0
             if self._ws is not None:
                 self._retired.append(self._ws)
-            self._ws = ops.new_workspace(self.device, nbytes)
+                grow = 2 * self._ws.numel()
+            self._ws = ops.new_workspace(self.device, max(nbytes, grow))
         return self._ws
 
     def set_length(self, seq: int, n: int) -> None:
@@ -225,6 +239,7 @@ class PagedKVCache:
         tmax = max(self.lengths)
         uniform = all(n == tmax for n in self.lengths)
         H = q.shape[2] if q_token_major else q.shape[1]
+        self._q_heads, self._q_len = max(self._q_heads, H), max(self._q_len, S)
         ws = self.workspace(ops.attention_workspace_bytes(1, B, H, self.kv_heads, S, self.head_dim, tmax))
         return ops.paged_attention(q, kp, vp, vs, self.block_table(), None if uniform else self.seq_lens_tensor(),
                                    tmax, q_token_major=q_token_major, out=out, workspace_tensor=ws,

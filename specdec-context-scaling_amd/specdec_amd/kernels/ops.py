@@ -33,7 +33,11 @@ _SCALE_MODES = {"div": _native.SCALE_DIV, "rcp": _native.SCALE_RCP}
 _BACKENDS = ("hip", "cuda")  # "cuda" is what reference call sites pass (patch.py:107)
 
 _WORKSPACES: dict = {}
-_RETIRED: list = []  # cached workspaces replaced by larger ones (a recorded graph may still use them)
+# Cached workspaces replaced by larger ones that a call recorded into a HIP graph used (the
+# graph still points at them).  A replacement is at least twice the size of the buffer it
+# replaces, so these hold at most as many bytes as the current workspace of their stream.
+_RETIRED: list = []
+_RECORDED = weakref.WeakSet()  # cached workspaces handed to a call while its stream was recording
 _READY: dict = {}  # id(tensor) -> weakref of workspaces whose sync prefix is known to be zero
 # SDV_CHECK_SYNC=1: every paged_attention call reads its workspace's failure count afterwards
 # and raises SdvError when a single-launch wait expired (synchronises; a debugging aid)
@@ -110,18 +114,25 @@ def _init_workspace(ws: torch.Tensor) -> None:
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """A cached uint8 workspace of at least nbytes on (device, current stream).
 
-    A cached buffer that is too small is replaced by a larger one but kept alive: a HIP graph
-    recorded with it still points at it.  Callers that record graphs should rather pass
-    their own buffer (``workspace_tensor``) and keep it for the graph's lifetime.
+    A cached buffer that is too small is replaced by one at least twice its size.  The old
+    buffer is freed, unless a call recorded into a HIP graph used it: the graph still points
+    at it, so it is kept alive (at most the current buffer's size in all, by the doubling).
+    Callers that record graphs should rather pass their own buffer (``workspace_tensor``)
+    and keep it for the graph's lifetime.
     """
     dev = torch.device(device)
     key = (dev, _stream(dev))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
+        grow = 0
         if ws is not None:
-            _RETIRED.append(ws)
-        ws = new_workspace(dev, max(nbytes, 1 << 20))
+            grow = 2 * ws.numel()
+            if ws in _RECORDED:
+                _RETIRED.append(ws)
+        ws = new_workspace(dev, max(nbytes, grow, 1 << 20))
         _WORKSPACES[key] = ws
+    if torch.cuda.is_current_stream_capturing():
+        _RECORDED.add(ws)
     return ws
 
 
@@ -133,27 +144,37 @@ def single_launch_workgroups(num_layers: int, batch: int, q_heads: int, kv_heads
                                                            max_seq_len))
 
 
-def workspace_status(ws: torch.Tensor) -> tuple[int, bool]:
+def _ws_args(ws: torch.Tensor | None):
+    """(pointer, bytes, stream) of a workspace; None: the current device's no-allocation scratch
+    (the workspace of sdv_paged_attention_noalloc), which the library names by a NULL pointer."""
+    if ws is None:
+        return None, 0, _stream(torch.device("cuda", torch.cuda.current_device()))
+    return _p(ws), ws.numel(), _stream(ws.device)
+
+
+def workspace_status(ws: torch.Tensor | None = None) -> tuple[int, bool]:
     """(failures, poisoned) of a workspace (sdv_attention_workspace_status; synchronises the
     current stream): failures = expired waits and refused calls of the single-launch path
     since the workspace was initialised; poisoned = graph-recorded calls are being refused
-    until reset_workspace()."""
+    until reset_workspace().  ws None: the no-allocation entry point's scratch on the current
+    device."""
     fail, poison = ctypes.c_uint32(0), ctypes.c_uint32(0)
-    _native.check(_native.load().sdv_attention_workspace_status(_p(ws), ws.numel(), ctypes.byref(fail),
-                                                                 ctypes.byref(poison), _stream(ws.device)),
+    ptr, n, st = _ws_args(ws)
+    _native.check(_native.load().sdv_attention_workspace_status(ptr, n, ctypes.byref(fail), ctypes.byref(poison), st),
                   "sdv_attention_workspace_status")
     return int(fail.value), bool(poison.value)
 
 
-def sync_errors(ws: torch.Tensor) -> int:
+def sync_errors(ws: torch.Tensor | None = None) -> int:
     """Expired waits and refused calls of the single-launch path recorded in a workspace
     (synchronises)."""
     return workspace_status(ws)[0]
 
 
-def check_workspace(ws: torch.Tensor) -> None:
+def check_workspace(ws: torch.Tensor | None = None) -> None:
     """Raise SdvError when a single-launch call on this workspace could not complete (its
-    outputs hold NaN where it failed); the reference raises every error (model_self.py:331-332)."""
+    outputs hold NaN where it failed); the reference raises every error (model_self.py:331-332).
+    ws None: the no-allocation entry point's scratch on the current device."""
     fail, poison = workspace_status(ws)
     if fail or poison:
         raise SdvError(f"single-launch attention: {fail} wait(s) expired or call(s) refused on this workspace"
@@ -161,9 +182,14 @@ def check_workspace(ws: torch.Tensor) -> None:
                        f"Call ops.reset_workspace() before recording new graphs on it", _native.SDV_ERR_HIP)
 
 
-def reset_workspace(ws: torch.Tensor) -> None:
-    """Zero a workspace's synchronisation area (clears the failure count and the graph poison)."""
-    _init_workspace(ws)
+def reset_workspace(ws: torch.Tensor | None = None) -> None:
+    """Zero a workspace's synchronisation area (clears the failure count and the graph poison).
+    ws None: the no-allocation entry point's scratch on the current device."""
+    if ws is not None:
+        _init_workspace(ws)
+        return
+    ptr, n, st = _ws_args(None)
+    _native.check(_native.load().sdv_attention_workspace_init(ptr, n, st), "sdv_attention_workspace_init")
 
 
 def set_wait_limit(polls: int) -> None:

@@ -102,18 +102,20 @@ def enable_fp8v(model) -> None:
         layer.self_attn.kv_format = "v_fp8"
 
 
-def reserve(cache_list, n_tokens: int) -> None:
-    """Page blocks (and the device block tables and workspaces) for n_tokens positions in every
-    layer of an engine cache, so that steps up to that length can be recorded into a HIP graph:
-    a recorded step then copies nothing from the host and allocates nothing (the reference's
-    graph experiments record the draft chain and the verify block at a fixed history length,
-    experiments/cuda_graph_local/draft_graph.py, verify_graph.py)."""
+def reserve(cache_list, n_tokens: int, q_len: int | None = None) -> None:
+    """Page blocks, device block tables and attention workspaces for n_tokens positions in
+    every layer of an engine cache, so that steps up to that length can be recorded into a
+    HIP graph: a recorded step then copies nothing from the host and allocates nothing (the
+    reference's graph experiments record the draft chain and the verify block at a fixed
+    history length, experiments/cuda_graph_local/draft_graph.py, verify_graph.py).  The
+    workspaces are sized for q_len new tokens per step (default: the largest step each layer
+    has run; PagedKVCache.reserve_all)."""
     for layer in cache_list:
         pages = layer.get("pages") if layer is not None else None
         if pages is None:
             continue
         pool = pages.pool
-        pool.reserve_all(n_tokens)
+        pool.reserve_all(n_tokens, q_len=q_len)
 
 
 def _accounting(m):

@@ -101,6 +101,51 @@ def test_append_attend_multi_layer_and_token_major(cuda_device):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+def test_append_attend_where_only_the_plain_call_fits_one_launch(cuda_device):
+    """24 layers x 4 sequences of the draft shape (14/2/64) at T = 8000: one 500-block item per
+    group.  The single launch holds that call with 8 wavefronts, but an appending call runs 16,
+    whose LDS for the wavefronts' p.V slots no longer fits beside 500 blocks of scores (items of
+    460-509 blocks are in that band for 7 query rows).  The append must then run as its own
+    kernel before whichever path serves the attention, leaving the same pages and output as the
+    two calls."""
+    announce("append+attend 24 layers x 4 seqs 14/2/64 at T=8000 (appending launch does not fit)")
+    L, B, kv, d, h, s, T0 = 24, 4, 2, 64, 14, 1, 7999
+    assert ops.single_launch_workgroups(L, B, h, kv, s, d, T0 + s) > 0
+    caches = []
+    for _ in range(2):
+        g = wl.gen(720, cuda_device)
+        c = PagedKVCache(kv, d, num_layers=L, batch=B, num_blocks=B * 500 + 8, device=cuda_device, seed=720,
+                         growable=False)
+        slots = None
+        for layer in range(L):
+            k = torch.randn((B * T0, kv, d), generator=g, device=cuda_device).to(torch.bfloat16)
+            v = torch.randn((B * T0, kv, d), generator=g, device=cuda_device).to(torch.bfloat16)
+            slots = c.prefill(layer, k, v, [T0] * B, slots)
+        caches.append(c)
+    sep, fused = caches
+    g = wl.gen(721, cuda_device)
+    k_new = torch.randn((L, B * s, kv, d), generator=g, device=cuda_device).to(torch.bfloat16)
+    v_new = (3 * torch.randn((L, B * s, kv, d), generator=g, device=cuda_device)).to(torch.bfloat16)
+    q = torch.randn((L, B, h, s, d), generator=g, device=cuda_device).to(torch.bfloat16)
+    for c in caches:
+        for b in range(B):
+            c.reserve(b, T0 + s)
+    slots = sep.slot_mapping([T0] * B, s)
+    for layer in range(L):
+        kp, vp, vs = sep.layer(layer)
+        ops.quant_append(v_new[layer], slots, kp, vp, vs, k_new[layer])
+    for c in caches:
+        for b in range(B):
+            c.lengths[b] = T0 + s
+    sl = sep.seq_lens_tensor()
+    want = ops.paged_attention(q, sep.k_pages, sep.v_pages, sep.v_scales, sep.block_table(), sl, T0 + s)
+    got = ops.paged_attention(q, fused.k_pages, fused.v_pages, fused.v_scales, fused.block_table(), sl, T0 + s,
+                              append=(k_new, v_new, None))
+    torch.cuda.synchronize()
+    assert _same_pages(sep, fused), "the new tokens were not written"
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 def test_append_attend_rejects_bad_shapes(cuda_device):
     c = PagedKVCache(2, 128, num_layers=1, batch=1, num_blocks=8, device=cuda_device, seed=1, growable=False)
     kp, vp, vs = c.layer(0)

@@ -136,7 +136,12 @@ def test_workspace_size_is_pure_host(lib):
 
 
 def test_workspace_init_validation(lib):
-    assert lib.sdv_attention_workspace_init(N, 1 << 21, N) == _native.SDV_ERR_NULL
+    # NULL names the current device's no-allocation scratch: with no device there is none
+    assert lib.sdv_attention_workspace_init(N, 1 << 21, N) in (_native.SDV_ERR_HIP, _native.SDV_OK)
+    f, p = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    assert lib.sdv_attention_workspace_status(N, 0, None, ctypes.byref(p), N) == _native.SDV_ERR_NULL
+    assert lib.sdv_attention_workspace_status(N, 0, ctypes.byref(f), ctypes.byref(p), N) in (_native.SDV_ERR_HIP,
+                                                                                          _native.SDV_OK)
     assert lib.sdv_attention_workspace_init(P, _native.SYNC_BYTES - 4, N) == _native.SDV_ERR_WORKSPACE
     assert lib.sdv_attention_workspace_init(ctypes.c_void_p(0x1010), 1 << 21, N) == _native.SDV_ERR_WORKSPACE
     # every attention workspace holds the synchronisation prefix

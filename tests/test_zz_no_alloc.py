@@ -31,15 +31,17 @@ def _cache(dev, layers, kv, d, t, seed):
     return cache
 
 
-def _noalloc(q, cache, t, out):
-    """One sdv_paged_attention_noalloc call (q (L, 1, H, S, D) or (1, H, S, D) for one layer)."""
+def _noalloc(q, cache, t, out, sl=None):
+    """One sdv_paged_attention_noalloc call (q (L, 1, H, S, D) or (1, H, S, D) for one layer);
+    sl: the lengths tensor (made here when None, which cannot happen inside a graph recording)."""
     lib = _native.load()
     layered = q.dim() == 5
     L = q.shape[0] if layered else 1
     B, H, S, D = q.shape[-4:]
     kp, vp, vs = (cache.k_pages, cache.v_pages, cache.v_scales) if layered else cache.layer(0)
     per = (lambda x: x[0].numel()) if layered else (lambda x: 0)
-    bt, sl = cache.block_table(), cache.seq_lens_tensor()
+    bt = cache.block_table()
+    sl = cache.seq_lens_tensor() if sl is None else sl
     nb = kp.shape[-5]
     return lib.sdv_paged_attention_noalloc(q.data_ptr(), kp.data_ptr(), vp.data_ptr(), vs.data_ptr(), nb,
                                            per(kp), per(vp), per(vs), bt.data_ptr(), bt.shape[1], sl.data_ptr(),
@@ -76,12 +78,15 @@ def test_noalloc_matches_workspace_entry_point(cuda_device):
     assert torch.equal(out3, ref1)
 
 
-@pytest.mark.parametrize("L,B,t,group", [(8, 32, 8192, False), (16, 32, 8192, True)])
+@pytest.mark.parametrize("L,B,t,group", [(12, 32, 2048, False), (32, 16, 8000, True)])
 def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device, L, B, t, group):
-    """Shapes whose workspace exceeds the scratch are rejected on the host and write nothing:
-    512 groups (three launches: scores, statistics and partials of every group) and 1024 groups
-    (the per-group kernel: 256 score rows per query row of the longest sequence)."""
+    """Shapes whose path needs more workspace than the scratch holds are rejected on the host
+    and write nothing: 768 groups with 2^17 tokens x KV heads per layer (too little work for one
+    single launch per layer: three launches, with scores, statistics and partials of every
+    group) and 1024 such groups (the per-group kernel: 256 score rows per query row of the
+    longest sequence)."""
     announce(f"noalloc: oversize shape L={L} B={B} T={t} rejected ({'per-group' if group else 'three-launch'})")
+    assert B * 2 * t < 1 << 18, "one single launch per layer would serve this shape"
     lib = _native.load()
     h, kv, d = 12, 2, 128
     need = lib.sdv_attention_workspace_size(L, B, h, kv, 1, d, t)
@@ -155,3 +160,80 @@ def test_noalloc_group_and_prefill_paths(cuda_device):
 
     announce("noalloc: prefill rows again")
     both(qp, pf, 3000, "prefill again")
+
+
+def test_noalloc_serves_per_layer_launches(cuda_device):
+    """8 layers x 32 sequences at 4K: more groups than one launch holds, but enough work per
+    layer for one single launch per layer, which needs only the synchronisation area -- so the
+    scratch serves it although the three-launch layout (sdv_attention_workspace_size) would not
+    fit; bitwise sdv_paged_attention's output."""
+    announce("noalloc: 8 layers x 32 x 12/2/128 T=4096 (one single launch per layer)")
+    lib = _native.load()
+    L, B, t = 8, 32, 4096
+    assert lib.sdv_attention_workspace_size(L, B, 12, 2, 1, 128, t) > _native.NOALLOC_MAX_WORKSPACE
+    assert lib.sdv_attention_single_launch(L, B, 12, 2, 1, 128, t) == 0
+    cache = _batch_cache(cuda_device, L, 2, 128, [t] * B, seed=930)
+    g = wl.gen(931, cuda_device)
+    q = torch.randn((L, B, 12, 1, 128), generator=g, device=cuda_device).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    assert _noalloc(q, cache, t, out) == _native.SDV_OK
+    want = ops.paged_attention(q, cache.k_pages, cache.v_pages, cache.v_scales, cache.block_table(),
+                               cache.seq_lens_tensor(), t)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want), "noalloc per-layer launches differ from sdv_paged_attention"
+
+
+@pytest.fixture()
+def _restore_wait_limit():
+    yield
+    ops.set_wait_limit(0)
+
+
+def test_noalloc_failure_state_is_readable_and_clearable(cuda_device, _restore_wait_limit):
+    """A graph-recorded noalloc call whose waits give up (a host-set wait bound: every kernel
+    still runs to its end) counts in, and poisons, the scratch; the status of the scratch (a
+    NULL workspace) shows it, later recorded calls are refused (NaN) until the scratch is
+    reset, and after the reset they are exact again."""
+    announce("noalloc: recorded call whose waits give up, scratch status, reset")
+    L, t = 4, 2048
+    cache = _cache(cuda_device, L, 2, 128, t, seed=940)
+    g = wl.gen(941, cuda_device)
+    q = torch.randn((L, 1, 12, 1, 128), generator=g, device=cuda_device).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    sl = cache.seq_lens_tensor()
+    cache.block_table()
+    assert _noalloc(q, cache, t, out, sl) == _native.SDV_OK  # outside capture first: takes the scratch
+    ref = ops.paged_attention(q, cache.k_pages, cache.v_pages, cache.v_scales, cache.block_table(),
+                              cache.seq_lens_tensor(), t)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    ops.reset_workspace(None)
+    assert ops.workspace_status(None) == (0, False)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    ops.set_wait_limit(0xFFFFFFFF)
+    bad = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(bad, stream=side):
+        rc_bad = _noalloc(q, cache, t, out, sl)
+    ops.set_wait_limit(0)
+    good = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(good, stream=side):
+        rc_good = _noalloc(q, cache, t, out, sl)
+    assert rc_bad == _native.SDV_OK and rc_good == _native.SDV_OK
+    bad.replay()
+    torch.cuda.synchronize()
+    fails, poisoned = ops.workspace_status(None)
+    print(f"recorded noalloc call whose waits give up: {fails} failures, poisoned={poisoned}")
+    assert fails > 0 and poisoned
+    with pytest.raises(ops.SdvError):
+        ops.check_workspace(None)
+    good.replay()                          # refused while poisoned: NaN everywhere, counted
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(out.float()).all())
+    assert ops.workspace_status(None)[0] > fails
+    ops.reset_workspace(None)
+    good.replay()
+    torch.cuda.synchronize()
+    assert ops.workspace_status(None) == (0, False)
+    assert torch.equal(out, ref), "a recorded call after the reset differs"

@@ -161,3 +161,127 @@ def test_planted_missing_sanitize_fails():
     p = plan(28, 32, 2, 1, 6, 32768)
     with pytest.raises(AssertionError):
         check_sequence(T, _table(nblk, nblk + 10, rng), nblk + 10, p, sanitize=False)
+
+
+# ---------------------------------------------------------------------------------------------
+# The `readfirstlane` question.  A build that marked pv_kernel's wavefront index wave-uniform
+# (wave = readfirstlane(tid >> 6)) gave NaN in some dimensions of every query row of a head on
+# four three-launch tests.  The two models below evaluate pv_compute's sanitizing inputs -- the
+# stage's fullness, each lane group's nvalid, the code byte masks, the scale and score masks --
+# once with the wavefront index taken per lane and once taken from the wavefront's first lane,
+# and check what reaches the MFMA byte by byte.
+
+E4M3FN_NAN = (0x7F, 0xFF)
+
+
+def wave_index(tid, uniform):
+    """tid >> 6 per lane, or (uniform) the first lane's value broadcast to the wavefront."""
+    return ((tid - tid % K_WAVE) >> 6) if uniform else (tid >> 6)
+
+
+def sanitize_masks(T, blk0, nb, my_pb, st, plant=0):
+    """pv_compute's masks for stage st of one wavefront, per lane group g: (needs, [(ok, blk,
+    code_keep[16], scale_keep[16], score_keep[16]) for g in 0..3]) exactly as the kernel forms
+    them: code bytes through the four 32-bit words' byte masks, the scale of token n through
+    n < nvalid, the BF16 scores through the 32-bit keep words (two tokens per word)."""
+    full_stages = min(nb, max(0, T // K_BLOCK - blk0)) >> 2
+    lanes = []
+    for g in range(4):
+        jj = 4 * st + g
+        pb = my_pb[jj if jj < K_WAVE else 0]
+        lanes.append((jj < nb and pb >= 0, blk0 + jj))
+    needs = (not (st < full_stages)) or any(not ok for ok, _ in lanes)
+    out = []
+    for ok, blk in lanes:
+        if not needs:
+            out.append((ok, blk, [True] * 16, [True] * 16, [True] * 16))
+            continue
+        nvalid = min(max(T - blk * K_BLOCK, 0), K_BLOCK) if ok else 0
+        nvalid_code = min(nvalid + plant, K_BLOCK)  # plant: a byte-mask mistake (tests only)
+        code = []
+        for w in range(4):
+            k = min(max(nvalid_code - 4 * w, 0), 4)
+            bmask = 0xFFFFFFFF if k >= 4 else (1 << (8 * k)) - 1
+            code += [((bmask >> (8 * i)) & 0xFF) == 0xFF for i in range(4)]
+        scale = [n < nvalid for n in range(16)]
+        score = []
+        for w in range(8):
+            keep = 0xFFFFFFFF if 2 * w + 1 < nvalid else (0x0000FFFF if 2 * w < nvalid else 0)
+            score += [(keep & 0xFFFF) == 0xFFFF, (keep >> 16) == 0xFFFF]
+        out.append((ok, blk, code, scale, score))
+    return needs, out
+
+
+def masks_of_sequence(T, table, num_blocks, p, uniform, plant=0):
+    """Every computed stage's masks for one sequence, the wavefront index taken per lane or
+    wave-uniformly (the workgroup's 256 threads: tid = 64 w + lane)."""
+    res = {}
+    for c in range(p["n_pv"]):
+        tok0 = c * p["pv_chunk"]
+        if tok0 >= T:
+            continue
+        for tid0 in range(0, K_WAVES * K_WAVE, K_WAVE):
+            waves = {wave_index(tid0 + lane, uniform) for lane in range(K_WAVE)}
+            assert len(waves) == 1, "a wavefront's lanes disagree on its index"
+            w = waves.pop()
+            blk0 = tok0 // K_BLOCK + w * p["pv_bpw"]
+            nb = max(0, min(p["pv_bpw"], -(-T // K_BLOCK) - blk0))
+            my_pb = [-1] * K_WAVE
+            for lane in range(nb):
+                pid = table[blk0 + lane]
+                my_pb[lane] = pid if 0 <= pid < num_blocks else -1
+            for st in range((nb + 3) >> 2):
+                res[(c, w, st)] = sanitize_masks(T, blk0, nb, my_pb, st, plant)
+    return res
+
+
+def _failing_shapes():
+    """The three-launch shapes of the four failing tests: the B=32 ragged batch of config 4
+    (lengths of test_multi_layer_batch32_ragged's seed) with tables holding holes, and short
+    sequences whose last stage is partial."""
+    rng = random.Random(41)
+    lens = [rng.randint(2048, 32768) for _ in range(32)]
+    p = plan(28, 32, 2, 1, 6, max(lens))
+    cases = []
+    for i, T in enumerate(lens[:8] + [17, 33, 1000, 18104]):
+        nblk = -(-T // K_BLOCK)
+        cases.append((T, _table(nblk, nblk + 64, rng, holes=i % 3), nblk + 64, p))
+    return cases
+
+
+def test_wave_uniform_index_gives_identical_sanitizing():
+    """The semantically neutral change is neutral for every sanitizing input: the masks of
+    every stage are the same whether the wavefront index is per lane or wave-uniform."""
+    for T, table, pool, p in _failing_shapes():
+        assert masks_of_sequence(T, table, pool, p, False) == masks_of_sequence(T, table, pool, p, True)
+
+
+def check_masks(cases, plant=0):
+    """Byte by byte: a slot that is not a token of the sequence (past T, or in a missing block
+    or one with an invalid page id) reaches the MFMA with code 0, scale 0 and score -inf, and
+    the stages left unsanitized hold tokens only; returns the number of non-token slots."""
+    non_token_slots = 0
+    for T, table, pool, p in cases:
+        for (needs, lanes) in masks_of_sequence(T, table, pool, p, True, plant).values():
+            for ok, blk, code, scale, score in lanes:
+                for i in range(16):
+                    if ok and blk * K_BLOCK + i < T:
+                        assert code[i] and scale[i] and score[i], "a token of the sequence was masked"
+                    else:
+                        non_token_slots += 1
+                        assert needs, "an unsanitized stage holds a slot that is not a token"
+                        assert not code[i] and not scale[i] and not score[i], "a non-token slot keeps a value"
+    return non_token_slots
+
+
+def test_every_non_token_slot_is_zeroed_before_the_mfma():
+    """So a NaN pattern left in an unwritten page (E4M3FN 0x7F / 0xFF) never meets p = 0 in the
+    MFMA.  The failing shapes do hold such slots: with their sanitizing skipped, a NaN code byte
+    among them gives NaN in its dimension for every query row, the recorded signature."""
+    assert check_masks(_failing_shapes()) > 0
+
+
+def test_planted_byte_mask_mistake_fails():
+    """A byte mask that keeps one token too many leaks a non-token code byte."""
+    with pytest.raises(AssertionError):
+        check_masks(_failing_shapes(), plant=1)

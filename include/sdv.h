@@ -164,7 +164,7 @@ int sdv_attention_set_wait_limit(uint32_t polls);
  * Which path sdv_paged_attention takes for these sizes on the current device: the number of
  * workgroups of the single-launch kernel, or 0 when another path serves the call (several
  * query-row groups, or a problem the device cannot hold at once: the persistent per-group
- * kernel for 1024 or more one-tile groups, else three launches).  A batch of 2..64 sequences
+ * kernel for 256 or more one-tile groups, else three launches).  A batch of 2..64 sequences
  * is taken to pass per-sequence lengths: its single launch uses every workgroup the device
  * holds and sizes each sequence's items from its length.  Queries the device's occupancy; no
  * launch.  No counterpart in the reference.

@@ -6,7 +6,16 @@
 //   p      = bf16( softmax_fp32(masked scores) )    -- normalised by the GLOBAL max and sum
 //   out    = bf16( p @ v_hat ),  v_hat = bf16(fp32(code) * scale)   (model_self.py:316-320)
 // Because p is rounded to BF16 after the global normalisation, a one-pass rescaled
-// online softmax cannot reproduce it; the work is split in three launches:
+// online softmax cannot reproduce it: every path takes the row statistics (max, sum) over the
+// whole sequence before it forms p.  The planner (make_plan, launch_all) picks one of:
+//   fused_kernel  one launch for the whole call: items of page blocks per (layer, sequence, KV
+//                 head) group, statistics and partials exchanged between workgroups through
+//                 the workspace's synchronisation area (also once per layer of a call too
+//                 large for one launch);
+//   group_kernel  256 or more one-tile groups the single launch cannot hold: persistent
+//                 workgroups that each compute whole groups;
+//   prefill_kernel many query rows (prefill chunks), two passes;
+// and the three launches, for the rest and for the profiling split (phase_mask):
 //
 //   qk_kernel     workgroup = 4 wavefronts = one chunk of page blocks of one (layer*batch,
 //                 KV head, query-row group).  Each wave runs q.k^T on MFMA
@@ -2153,7 +2162,12 @@ constexpr int kGroupWaves = 8;
 constexpr int kGroupGrid = 256;          // workgroups (one per CU of the MI355X)
 constexpr int kGroupMaxBlocks = 4096;    // page ids of one group staged in LDS: T <= 65536
 constexpr int kGroupSortMax = 1024;      // batches up to this size are ordered by length
-constexpr int kGroupMinGroups = 1024;    // fewer groups: the three-launch path spreads them wider
+// Fewest groups this kernel takes: one per workgroup.  Between that and the 1,024 groups it
+// once started at (one-tile groups the single launch cannot hold at once, with too little work
+// per layer for one single launch per layer), it beats the three launches on every shape
+// measured: one layer of 160 ragged sequences up to 3K tokens 63.1 -> 50.8 us, 300 x 2K
+// 112 -> 108 us, 480 ragged up to 4K 214.6 -> 181.9 us, 2 layers x 200 x 1K 85.5 -> 77.0 us.
+constexpr int kGroupMinGroups = kGroupGrid;
 // K blocks and V stages (4 blocks) in flight per wavefront.  Deeper rings measured no faster on
 // config 4 (K 3-4, V 3: 2.55-2.60 ms against 2.54 ms)
 constexpr int kGroupKRing = 2;

@@ -139,10 +139,11 @@ def test_config4_batch32_ragged(cuda_device, split):
     print("config4 worst rel_l2", worst)
 
 
-def test_three_launch_many_groups(cuda_device):
-    """More one-tile groups than the device holds at once but fewer than the per-group kernel
-    takes (160 sequences x 2 KV heads): the planner's three launches, every sequence checked."""
-    announce("attn three launches, 160 ragged sequences")
+def test_many_groups_band(cuda_device):
+    """More one-tile groups than the single launch holds at once, one layer (160 sequences x 2
+    KV heads): the persistent per-group kernel, which took this band over from the three
+    launches; every sequence checked."""
+    announce("attn per-group kernel, 160 ragged sequences")
     g = np.random.default_rng(77)
     lens = [int(x) for x in g.integers(17, 3000, size=160)]
     assert ops.single_launch_workgroups(1, len(lens), 12, 2, 1, 128, max(lens)) == 0

@@ -1,4 +1,4 @@
-"""The persistent per-group kernel (csrc/sdv_attn.hip, group_kernel): calls with 1024 or more
+"""The persistent per-group kernel (csrc/sdv_attn.hip, group_kernel): calls with 256 or more
 (layer, sequence, KV head) groups of one row tile -- config 4's 28 layers x 32 ragged
 sequences is one -- take it instead of the three-launch path.  Each group is computed whole
 by one workgroup, claimed longest sequence first from a counter that the last workgroup

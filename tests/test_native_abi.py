@@ -178,13 +178,19 @@ def test_phase_trace_stays_out_of_the_product_library(lib):
 
 
 def test_group_shapes_workspace_and_no_split(lib):
-    """A batch of 1024 or more one-tile groups runs in one launch of the per-group kernel: its
-    workspace is the synchronisation prefix plus 256 score rows per query row of the longest
-    sequence, and the profiling split refuses it (before any launch)."""
+    """A batch of 256 or more one-tile groups (one per workgroup of the per-group kernel) that
+    no single launch serves runs in one launch of the per-group kernel: its workspace is the
+    synchronisation prefix plus 256 score rows per query row of the longest sequence, and the
+    profiling split refuses it (before any launch)."""
     L, B, H, KV, D, T = 28, 32, 12, 2, 128, 32768          # 1792 groups of 6 rows
     need = lib.sdv_attention_workspace_size(L, B, H, KV, 1, D, T)
     assert need == _native.SYNC_BYTES + 256 * (H // KV) * T * 2
-    assert lib.sdv_attention_workspace_size(L, 8, H, KV, 1, D, T) > need   # 448 groups: three launches
+    # 448 groups, at least one per workgroup: the per-group kernel
+    assert lib.sdv_attention_workspace_size(L, 8, H, KV, 1, D, T) == need
+    # 112 groups, fewer than one per workgroup: the three launches' layout (scores of every
+    # group: 112 x 6 x 32768 x 2 bytes and more), not the per-group kernel's
+    three = lib.sdv_attention_workspace_size(L, 2, H, KV, 1, D, T)
+    assert three != need and three > _native.SYNC_BYTES + 112 * (H // KV) * T * 2
 
     def phases(mask):
         return lib.sdv_paged_attention_phases(P, P, P, P, 8, 1 << 30, 1 << 30, 1 << 30, P, T // 16, P, L, B, H,

@@ -78,19 +78,20 @@ def test_noalloc_matches_workspace_entry_point(cuda_device):
     assert torch.equal(out3, ref1)
 
 
-@pytest.mark.parametrize("L,B,t,group", [(12, 32, 2048, False), (32, 16, 8000, True)])
-def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device, L, B, t, group):
+@pytest.mark.parametrize("L,B,s,t,group", [(1, 160, 5, 4096, False), (32, 16, 1, 8000, True)])
+def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device, L, B, s, t, group):
     """Shapes whose path needs more workspace than the scratch holds are rejected on the host
-    and write nothing: 768 groups with 2^17 tokens x KV heads per layer (too little work for one
-    single launch per layer: three launches, with scores, statistics and partials of every
-    group) and 1024 such groups (the per-group kernel: 256 score rows per query row of the
-    longest sequence)."""
-    announce(f"noalloc: oversize shape L={L} B={B} T={t} rejected ({'per-group' if group else 'three-launch'})")
-    assert B * 2 * t < 1 << 18, "one single launch per layer would serve this shape"
+    and write nothing: 320 groups of two row tiles (verify rows, more groups than the single
+    launch holds: three launches, with scores, statistics and partials of every group) and
+    1024 one-tile groups with 2^18 - 6144 tokens x KV heads per layer (too little work for one
+    single launch per layer: the per-group kernel, 256 score rows per query row of the longest
+    sequence)."""
+    announce(f"noalloc: oversize shape L={L} B={B} S={s} T={t} rejected ({'per-group' if group else 'three-launch'})")
+    assert L == 1 or B * 2 * t < 1 << 18, "one single launch per layer would serve this shape"
     lib = _native.load()
     h, kv, d = 12, 2, 128
-    need = lib.sdv_attention_workspace_size(L, B, h, kv, 1, d, t)
-    assert lib.sdv_attention_single_launch(L, B, h, kv, 1, d, t) == 0
+    need = lib.sdv_attention_workspace_size(L, B, h, kv, s, d, t)
+    assert lib.sdv_attention_single_launch(L, B, h, kv, s, d, t) == 0
     assert need > _native.NOALLOC_MAX_WORKSPACE
     if group:
         assert need == _native.SYNC_BYTES + 256 * (h // kv) * t * 2
@@ -99,7 +100,9 @@ def test_noalloc_rejects_what_the_scratch_cannot_hold(cuda_device, L, B, t, grou
     for b in range(B):
         cache.reserve(b, t)
         cache.set_length(b, t)
-    q = torch.zeros((L, B, h, 1, d), dtype=torch.bfloat16, device=cuda_device)
+    q = torch.zeros((L, B, h, s, d), dtype=torch.bfloat16, device=cuda_device)
+    if L == 1:
+        q = q[0]
     out = torch.full_like(q, 7.0)
     assert _noalloc(q, cache, t, out) == _native.SDV_ERR_WORKSPACE
     torch.cuda.synchronize()
@@ -163,13 +166,14 @@ def test_noalloc_group_and_prefill_paths(cuda_device):
 
 
 def test_noalloc_serves_per_layer_launches(cuda_device):
-    """8 layers x 32 sequences at 4K: more groups than one launch holds, but enough work per
+    """8 layers x 32 sequences at 12K: more groups than one launch holds, but enough work per
     layer for one single launch per layer, which needs only the synchronisation area -- so the
-    scratch serves it although the three-launch layout (sdv_attention_workspace_size) would not
-    fit; bitwise sdv_paged_attention's output."""
-    announce("noalloc: 8 layers x 32 x 12/2/128 T=4096 (one single launch per layer)")
+    scratch serves it although the layout of the per-group kernel (sdv_attention_workspace_size:
+    a 12K row of scores per query row for each of its 256 workgroups) would not fit; bitwise
+    sdv_paged_attention's output."""
+    announce("noalloc: 8 layers x 32 x 12/2/128 T=12288 (one single launch per layer)")
     lib = _native.load()
-    L, B, t = 8, 32, 4096
+    L, B, t = 8, 32, 12288
     assert lib.sdv_attention_workspace_size(L, B, 12, 2, 1, 128, t) > _native.NOALLOC_MAX_WORKSPACE
     assert lib.sdv_attention_single_launch(L, B, 12, 2, 1, 128, t) == 0
     cache = _batch_cache(cuda_device, L, 2, 128, [t] * B, seed=930)

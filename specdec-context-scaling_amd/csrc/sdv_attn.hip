@@ -87,6 +87,14 @@ struct AttnArgs {
   uint32_t spin_limit;
   // prefill pass 2: key parts per row group (1: each workgroup writes its rows' outputs itself)
   int pf_parts;
+  // prefill pass 1: key parts per row group (the (max, sum) of each, per row, in stats)
+  int pf_split;
+  // prefill: V dequantized once per call by pass 1 for pass 2.  Per (layer, sequence, KV head)
+  // group, vh_stages stages of two page blocks, each D/16 dimension tiles x 64 lanes x 16 bytes
+  // in the lane order of the p.V MFMA's A operand (lane (g, n): dimension dt*16 + n, tokens
+  // 4g..4g+3 of the first block, then of the second)
+  uint4* vhat;
+  int vh_stages;
 };
 
 __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
@@ -1732,68 +1740,76 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // ---------------------------------------------------------------------------- prefill
 // Shapes with more query rows than one row-tile group holds (R = G*S > 64: prefill and
 // chunked-prefill blocks, model_self.py:471-504, 637-648) in two launches whose workspace holds
-// only the per-row (max, sum) of each key part -- 64 bytes per row -- instead of the O(S*T)
-// scores:
-//   pass 1  each wavefront takes 16 rows (one MFMA row tile) and streams one of the
-//           kPrefillSplit parts of the page blocks its rows can see (one workgroup per part):
-//           S^T = K Q^T on MFMA (the K page is the A operand, the rows the B operand), scores
+// the per-row (max, sum) of each key part -- 8 bytes per row and part -- and V dequantized once
+// (2 bytes per key and dimension of each KV head) instead of the O(S*T) scores:
+//   pass 1  each wavefront takes 32 rows (two MFMA row tiles) and streams one part of the page
+//           blocks its rows can see (one workgroup per part): S^T = K Q^T on MFMA (the K page is
+//           the A operand, the rows the B operand; one K operand serves both tiles), scores
 //           rounded to BF16 twice, offset-causal mask, online (max, sum) per lane, merged over
-//           the lane groups into the part's (max, sum) per row; pass 2 merges the parts in
-//           part order into (M, L).
-//   pass 2  the workgroup streams the blocks of its rows again, two at a time; each wavefront
-//           recomputes its rows' BF16 scores and forms p = bf16(exp(s - M) / L) in registers.
-//           A lane's S^T fragment (row n, tokens 4g..4g+3 of each of the two blocks) is exactly
-//           the B operand of O^T = V_hat^T P^T with those 8 tokens as its k-slots, so the A
-//           operand is the matching 4-byte words of the dimension-major V pages (one wave load
-//           covers 16 dimensions x 16 tokens of a page, contiguous), dequantized as
-//           bf16(fp32(code) * scale).  That operand does not depend on the rows: each wavefront
-//           dequantizes a quarter of the dimension tiles into LDS (two buffers, one barrier per
-//           stage) and reads all of them from there.  O^T accumulates in fp32 and leaves as
-//           BF16, four dimensions of one row per lane.
+//           the lane groups into the part's (max, sum) per row.  The launch also dequantizes
+//           V, each stage of two blocks once, as bf16(fp32(code) * scale) in the lane order of
+//           pass 2's MFMA operand.
+//   pass 2  merges the parts in part order into (M, L); each wavefront (32 rows) streams its
+//           part of the blocks again, two at a time, recomputes its rows' BF16 scores and forms
+//           p = bf16(exp(s - M) / L) in registers.  A lane's S^T fragment (row n, tokens
+//           4g..4g+3 of each of the two blocks) is exactly the B operand of O^T = V_hat^T P^T
+//           with those 8 tokens as its k-slots; the A operand is the stage's dequantized V,
+//           16 bytes per lane and dimension tile, loaded like K.  No wavefront waits for
+//           another.  O^T accumulates in fp32; the parts' partials are summed in part order
+//           by the last part to finish, and leave as BF16, four dimensions of one row per lane.
 // Rows are head-major (row r: head r / S, token r % S) as in the other kernels.  Row r sees
 // keys j <= T - S + r % S (the eager mask); T >= S is the caller's contract (the S new tokens
 // are part of the context), and a row that sees no key outputs 0.  The page ids of the
-// workgroup's blocks are staged in LDS, kPrefillWindow at a time.
-// One MFMA row tile (16 rows) per wavefront: twice the wavefronts of two tiles, which pass 1
-// needs (2048 x 8192, 12/2/128: 296-311 -> 226-242 us); pass 2 then shares the dequantized V
-// of each stage through LDS (per wavefront it would cost twice the conversions: 588-604 us).
-constexpr int kPrefillRows = 16;   // query rows per wavefront (16 per MFMA row tile)
+// workgroup's blocks are staged in LDS, kPrefillWindow at a time.  Measured steps (2048 x 8192,
+// 12/2/128 and 14/2/64, both passes): 451 / 324 us with 16 rows per wavefront and V dequantized
+// per stage into LDS by the workgroup; scalar branches for the unmasked stages 442 / 281;
+// two row tiles in pass 1 382 / 263; two in pass 2 350 / 235; V dequantized by pass 1 and
+// MFMA results in VGPRs 332 / 218; 16-byte part slots and key parts per launch size 303 / 196.
+constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
 constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
 // pass 1: stages (two blocks each) in flight per wavefront (3 measured equal, 4 slower)
 constexpr int kPrefillRing = 2;
-// Pass 1 splits each row group's keys in 8 parts, one workgroup each (eight times the
-// wavefronts; pass 2 merges the parts' (max, sum) in part order): 2048 x 8192, pass 1 with one
-// part 256 / 218 us (12/2/128 / 14/2/64), 2 parts 167-178 / 169-175, 4 parts 163-175 /
-// 136-146, 8 parts 160-172 / 120-129 us (the 4-part grid ran 1.5 rounds of resident
-// wavefronts, the 8-part grid runs 3)
-constexpr int kPrefillSplit = 8;
-// Pass 2: workgroups per row group (key parts; the last part to finish sums them): two (2048 x
-// 8192, 14/2/64: pass 2 277 -> 221 us; 12/2/128 with its one-stage ring below: 354-372 ->
-// 297-317 us)
-constexpr int prefill_parts(int D) { return 2; }
 constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
+// Pass 1: row tiles per wavefront (each K operand it loads serves this many tiles; 2048 x 8192,
+// pass 1 with one tile 158 / 93 us (12/2/128 / 14/2/64), with two 101 / 77 us)
+constexpr int kPass1Tiles = 2;
+// Pass 2: row tiles per wavefront, and the rows of a workgroup (a row group: its part slots,
+// its counter)
+constexpr int kPass2Tiles = 2;
+constexpr int kPass2Rows = kPass2Tiles * kPrefillRows * kPrefillWaves;
+// Both passes split each row group's keys in parts, one workgroup each (pass 2 merges pass 1's
+// (max, sum) in part order; the last pass-2 part to finish sums the parts' outputs), as many
+// as bring the launch to about this many workgroups, at most kPrefillMaxParts and none under
+// 8 blocks.  Pass 1: 2048 x 8192 in 8 parts (12/2/128: 101 us, 16 parts 108 us; 14/2/64: 74 us,
+// 11 parts 83 us, 6 parts 80 us);
+// pass 2: one round, two wavefronts per SIMD for head_dim 128 and three for 64 (2048 x 8192: 2
+// parts 12/2/128, 3 parts 14/2/64).
+constexpr int pass1_workgroups(int D) { return D == 128 ? 1536 : 1792; }
+constexpr int pass2_workgroups(int D) { return D == 128 ? 512 : 768; }
+constexpr int kPrefillMaxParts = 64;
+// pass 2: the last part to finish adds every part's slot of its row group
+constexpr int kPrefillMaxParts2 = 8;
 
 template <int D, bool OUT>
 __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a) {
-  constexpr int KK = D / 32, DT = D / 16, NT = kPrefillRows / 16;
-  constexpr int DTW = DT / kPrefillWaves;  // pass 2: dimension tiles of V each wavefront dequantizes
+  // row tiles of 16 rows per wavefront: two in pass 1 (each K operand serves 32 rows), one in
+  // pass 2
+  constexpr int KK = D / 32, DT = D / 16, NT = OUT ? kPass2Tiles : kPass1Tiles, ROWS = NT * 16;
+  constexpr int DTW = DT / kPrefillWaves;  // pass 1: dimension tiles of V each wavefront dequantizes
   static_assert(DTW * kPrefillWaves == DT, "the wavefronts share the dimension tiles evenly");
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   __shared__ int lpb[kPrefillWindow];
   __shared__ int s_kend;
-  // pass 2: the dequantized V operand of a stage (it does not depend on the query rows, so the
-  // workgroup forms it once): [buffer][dimension tile][lane], 16 bytes each
-  __shared__ uint4 lv[OUT ? 2 : 1][OUT ? DT : 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int kvh = blockIdx.y, zb = blockIdx.z, b = zb % a.B, layer = zb / a.B;
   const int T = seq_len_of(a, b);
   const int grp = zb * a.KV + kvh;
-  // the keys of a row group are split in parts, one workgroup each: kPrefillSplit in pass 1,
+  // the keys of a row group are split in parts, one workgroup each: a.pf_split in pass 1,
   // a.pf_parts in pass 2
-  const int nparts = OUT ? a.pf_parts : kPrefillSplit;
+  const int nparts = OUT ? a.pf_parts : a.pf_split;
   const int split = (int)(blockIdx.x % nparts);
   const int rgi = (int)(blockIdx.x / nparts);
-  const int row0 = (rgi * kPrefillWaves + wave) * kPrefillRows;
+  const int row0 = (rgi * kPrefillWaves + wave) * ROWS;
 
   // this lane's rows (row tile nt: row row0 + nt*16 + n): q operand and last visible key
   bf16x8 qop[NT][KK];
@@ -1810,7 +1826,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     lim[nt] = rv[nt] ? min(T - 1, T - a.S + si) : -1;
   }
   // blocks this wavefront streams (keys 0 .. max lim) and the smallest lim of its rows (every
-  // key up to it is seen by every row: no mask inside a block below it)
+  // key up to it is seen by every row: the blocks below nfull need no mask).  Both are
+  // wave-uniform and kept in scalar registers, so that every branch on them below is a
+  // scalar branch rather than a change of the execution mask.
   int kend = 0, kmin = INT_MAX;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -1822,22 +1840,52 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     kend = max(kend, __shfl_xor(kend, off));
     kmin = min(kmin, __shfl_xor(kmin, off));
   }
-  const int nblk = (kend + kBlock - 1) >> 4;  // wave-uniform
+  const int nblk = __builtin_amdgcn_readfirstlane((kend + kBlock - 1) >> 4);
+  const int nfull = __builtin_amdgcn_readfirstlane(kmin == INT_MAX ? 0 : max(0, (kmin + 1) >> 4));
   if (tid == 0) s_kend = 0;
   __syncthreads();
   if (lane == 0) atomicMax(&s_kend, nblk);
   __syncthreads();
-  const int nblk_wg = s_kend;
+  const int nblk_wg = __builtin_amdgcn_readfirstlane(s_kend);
 
-  const uint16_t* kbase = a.k_pages + layer * a.k_ls + (int64_t)lane * 8;
-  const uint8_t* vlayer = a.v_pages + layer * a.v_ls;
-  const float* slayer = a.v_scales + layer * a.s_ls;
+  // page addressing: a page id's base is scalar (this layer and KV head), the lane's offset a
+  // 32-bit vector offset
+  const uint16_t* klayer = a.k_pages + layer * a.k_ls + (int64_t)kvh * (kBlock * D);
+  const uint8_t* vlayer = a.v_pages + layer * a.v_ls + (int64_t)kvh * (D * kBlock);
+  const float* slayer = a.v_scales + layer * a.s_ls + (int64_t)kvh * kBlock;
+  const int64_t kpage = (int64_t)a.KV * (kBlock * D);  // K elements, V bytes per page id
+  const int64_t spage = (int64_t)a.KV * kBlock;        // scales per page id
+  const unsigned koff = (unsigned)lane * 8u;
+  const unsigned voff = (unsigned)((wave * DTW * 16 + n) * kBlock + 4 * g);
   const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
-  float2* st = a.stats + (int64_t)grp * a.R * kPrefillSplit;  // row r, part k: st[r * kPrefillSplit + k]
+  float2* st = a.stats + (int64_t)grp * a.R * a.pf_split;  // row r, pass-1 part k: st[r * a.pf_split + k]
   // this workgroup's key blocks: part `split` of [0, nblk_wg)
   const int part = (((nblk_wg + nparts - 1) / nparts) + 1) & ~1;  // even: whole stages
   const int blo = min(nblk_wg, split * part);
   const int bhi = min(nblk_wg, blo + part);
+
+  // Scores in the eager units: bf16(bf16(x) / sqrt(D)).  For head_dim 64 the divisor is 8 and
+  // bf16(x) * 0.125 is exact, so the scores are kept as bf16(x) -- one rounding -- and the
+  // factor 0.125 goes into the row max (exact) and into the exponent's coefficient
+  // (kLog2e * 0.125 is exact, so fma(bf16(x), kLog2e * 0.125, c) is bit for bit
+  // fma(bf16(x) * 0.125, kLog2e, c)).
+  constexpr float kUnit = D == 64 ? 0.125f : 1.0f;
+  constexpr float kExpCoef = kLog2e * kUnit;
+  const float csc = a.inv_sqrt_d;
+  auto eager4 = [&](const f32x4& s, float* y) {
+    if constexpr (D == 64) {
+      const uint32_t r01 = pack_bf16x2(s[0], s[1]), r23 = pack_bf16x2(s[2], s[3]);
+      y[0] = bf16_lo(r01);
+      y[1] = bf16_hi(r01);
+      y[2] = bf16_lo(r23);
+      y[3] = bf16_hi(r23);
+    } else {
+      float t[4];
+      round_scaled4(s[0], s[1], s[2], s[3], csc, t);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = t[i];
+    }
+  };
 
   float m_run[NT], l_run[NT];   // pass 1: running max and sum
   float nml[NT], invl[NT];      // pass 2: -M log2 e and 1/L per row
@@ -1850,10 +1898,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     invl[nt] = 0.0f;
     if (OUT && rv[nt]) {
       // (M, L) of the row: its parts merged in part order
-      const float2* sr = st + (int64_t)(row0 + nt * 16 + n) * kPrefillSplit;
+      const float2* sr = st + (int64_t)(row0 + nt * 16 + n) * a.pf_split;
       float m = sr[0].x, l = sr[0].y;
-#pragma unroll
-      for (int k = 1; k < kPrefillSplit; ++k) merge_fast(m, l, sr[k].x, sr[k].y);
+      for (int k = 1; k < a.pf_split; ++k) merge_fast(m, l, sr[k].x, sr[k].y);
       if (l > 0.0f) {
         nml[nt] = -m * kLog2e;
         invl[nt] = 1.0f / l;
@@ -1863,21 +1910,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     for (int dt = 0; dt < DT; ++dt) acc[dt][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // A stage is two consecutive blocks u = 0, 1: K operands, page ids and, for pass 2, the V
-  // words of this wavefront's dimension tiles wave*DTW .. (lane (g, n): dimension dt*16 + n,
-  // tokens 4g..4g+3) and the four scales of those tokens.
-  // Pass 2 keeps one stage in registers and issues the next stage's loads inside the stage,
-  // once its registers are dead (106 VGPRs + 36 AGPRs for head_dim 128: three wavefronts per
-  // SIMD, two with two stages; 82 + 20 for head_dim 64).  2048 x 8192, pass 2: 298-301 ->
-  // 290-295 us (12/2/128), 217-220 -> 211-213 us (14/2/64, where two stages loaded after the
-  // stage's products measured 217-220 and one 220-226 us).
+  // A stage is two consecutive blocks u = 0, 1: their page ids and K operands and, for pass 2,
+  // the stage's dequantized V operand (D/16 tiles, written by pass 1).  Pass 1 keeps
+  // kPrefillRing stages in flight; pass 2 keeps one, and loads the next stage's K as soon as
+  // the stage's q.k^T products are issued and its V operand after the p.V products.
   constexpr int RING = OUT ? 1 : kPrefillRing;
   struct Stage {
     bf16x8 k[2][KK];
-    uint32_t v[2][OUT ? DTW : 1];
-    float4 sc[2];
+    bf16x8 vh[OUT ? DT : 1];
     int pb[2];
   };
+  const uint4* vh_grp = a.vhat + (int64_t)grp * a.vh_stages * (DT * 64) + lane;
   for (int w0 = blo; w0 < bhi; w0 += kPrefillWindow) {  // workgroup-uniform
     const int wn = min(kPrefillWindow, bhi - w0);
     __syncthreads();  // the previous window's page ids are no longer read
@@ -1888,67 +1931,60 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     __syncthreads();
     const int jn = max(0, min(nblk - w0, wn));  // this wavefront's blocks in the window
     // a block past jn (or invalid) reads page 0, which is always allocated; it is never used
-    auto load_stage = [&](int s2, Stage& x) {
+    auto load_k = [&](int s2, Stage& x) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int jb = 2 * s2 + u;
-        x.pb[u] = jb < (OUT ? wn : jn) ? lpb[jb] : -1;
-        const int64_t page = (int64_t)max(x.pb[u], 0) * a.KV + kvh;
-        const uint16_t* kp = kbase + page * (kBlock * D);
+        int pb = -1;
+        if (jb < jn) pb = __builtin_amdgcn_readfirstlane(lpb[jb]);  // the same word in every lane
+        x.pb[u] = pb;
+        const int64_t pg = max(pb, 0);
+        const uint16_t* kp = klayer + pg * kpage;
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) x.k[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + kk * 512));
-        if constexpr (OUT) {
-          const uint8_t* vp = vlayer + (page * D + wave * DTW * 16 + n) * kBlock + 4 * g;
-#pragma unroll
-          for (int dtl = 0; dtl < DTW; ++dtl) x.v[u][dtl] = *reinterpret_cast<const uint32_t*>(vp + dtl * 16 * kBlock);
-          x.sc[u] = *reinterpret_cast<const float4*>(slayer + page * kBlock + 4 * g);
-        }
+        for (int kk = 0; kk < KK; ++kk) x.k[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + (koff + kk * 512u)));
       }
+    };
+    // the stage's V operand; a stage past the group's (a reload after the last stage) reads
+    // the last one and is not used
+    auto load_vh = [&](int s2, Stage& x) {
+      const int sg = min((w0 >> 1) + s2, a.vh_stages - 1);
+      const uint4* src = vh_grp + (int64_t)sg * (DT * 64);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) x.vh[dt] = __builtin_bit_cast(bf16x8, src[dt * 64]);
+    };
+    auto qk = [&](const Stage& x, int u, int nt) {
+      f32x4 s = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.k[u][kk], qop[nt][kk], s, 0, 0, 0);
+      return s;
     };
     auto compute_stage = [&](int s2, Stage& x) {
       const int jg0 = w0 + 2 * s2;  // global block of u = 0
-      bf16x8 pop[NT];
-      uint32_t pw[NT][4];           // packed BF16 probabilities: u = 0 in words 0-1, u = 1 in 2-3
-      float sv[NT][8];              // pass 1: the stage's scores, u = 0 in 0-3, u = 1 in 4-7
-      const bool mine = 2 * s2 < jn;  // wave-uniform: the stage has keys this wavefront's rows see
-      // every key of the stage exists, is valid and is seen by every row: no mask
-      const bool full = 2 * s2 + 1 < jn && x.pb[0] >= 0 && x.pb[1] >= 0 && (jg0 + 2) * kBlock - 1 <= kmin;
+      // scalar: every key of the stage exists, is valid and is seen by every row
+      const bool full = jg0 + 2 <= nfull && 2 * s2 + 1 < jn && x.pb[0] >= 0 && x.pb[1] >= 0;
+      float y[NT][8];  // the stage's scores (in units of kUnit), u = 0 in 0-3, u = 1 in 4-7
+      if (full) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const bool have = 2 * s2 + u < jn;  // wave-uniform
-        if (!have) {
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            pw[nt][2 * u] = pw[nt][2 * u + 1] = 0u;
+          for (int nt = 0; nt < NT; ++nt) eager4(qk(x, u, nt), y[nt] + 4 * u);
+      } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sv[nt][4 * u + i] = -INFINITY;
-          }
-          continue;
-        }
-        const int t0 = (jg0 + u) * kBlock + 4 * g;
-        const bool blk_ok = x.pb[u] >= 0;
+        for (int u = 0; u < 2; ++u) {
+          if (2 * s2 + u < jn) {  // scalar
+            const int t0 = (jg0 + u) * kBlock + 4 * g;
+            const bool blk_ok = x.pb[u] >= 0;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          f32x4 sacc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            for (int nt = 0; nt < NT; ++nt) {
+              eager4(qk(x, u, nt), y[nt] + 4 * u);
 #pragma unroll
-          for (int kk = 0; kk < KK; ++kk) sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.k[u][kk], qop[nt][kk], sacc, 0, 0, 0);
-          float s4[4];
-          float y[4];
-          round_scaled4(sacc[0], sacc[1], sacc[2], sacc[3], a.inv_sqrt_d, y);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float v = y[i];
-            s4[i] = (full || (blk_ok && t0 + i <= lim[nt])) ? v : -INFINITY;
-          }
-          if constexpr (!OUT) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sv[nt][4 * u + i] = s4[i];
+              for (int i = 0; i < 4; ++i) y[nt][4 * u + i] = (blk_ok && t0 + i <= lim[nt]) ? y[nt][4 * u + i] : -INFINITY;
+            }
           } else {
-            float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s4[i], kLog2e, nml[nt])) * invl[nt];
-            pw[nt][2 * u] = pack_bf16x2(p[0], p[1]);
-            pw[nt][2 * u + 1] = pack_bf16x2(p[2], p[3]);
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) y[nt][4 * u + i] = -INFINITY;
           }
         }
       }
@@ -1958,93 +1994,106 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
         // exactly 1 while the max stays (the one-FMA form exp2(m_old log2 e - RN(m_new log2 e))
         // is off by the product's rounding on every update, and L drifted by ~1e-5 at T = 8192:
         // rel-L2 7e-4 against eager).  A lane sums at most T/32 terms of at most 1 each, so the
-        // plain fp32 sum is within ~1e-5 relative of the exact one.
+        // plain fp32 sum is within ~1e-5 relative of the exact one.  A stage without masked keys
+        // has a finite max, and exp2(-inf) = 0 covers the first update.
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-          const float mt = fmaxf(fmaxf(fmaxf(sv[nt][0], sv[nt][1]), fmaxf(sv[nt][2], sv[nt][3])),
-                                 fmaxf(fmaxf(sv[nt][4], sv[nt][5]), fmaxf(sv[nt][6], sv[nt][7])));
-          if (mt != -INFINITY) {
+          const float* yt = y[nt];
+          const float mt =
+              fmaxf(fmaxf(fmaxf(yt[0], yt[1]), fmaxf(yt[2], yt[3])), fmaxf(fmaxf(yt[4], yt[5]), fmaxf(yt[6], yt[7]))) * kUnit;
+          if (full || mt != -INFINITY) {
 #pragma clang fp contract(off)
             const float mn = fmaxf(m_run[nt], mt), nm = -mn * kLog2e;
-            const float f = (m_run[nt] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
+            const float f = __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
             float e[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[nt][i], kLog2e, nm));
-            const float x = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-            l_run[nt] = l_run[nt] * f + x;
+            for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(yt[i], kExpCoef, nm));
+            const float xs = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+            l_run[nt] = l_run[nt] * f + xs;
             m_run[nt] = mn;
           }
         }
-      }
-      if constexpr (OUT) {
+      } else {
+        load_k(s2 + 1, x);  // the K registers are free once the products are issued
+        bf16x8 pop[NT];     // packed BF16 probabilities: u = 0 in elements 0-3, u = 1 in 4-7
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[nt][0], pw[nt][1], pw[nt][2], pw[nt][3]));
-        // this wavefront's dimension tiles of the stage's V operand, dequantized once for the
-        // workgroup.  Codes and scales of tokens that are not in the sequence (past T, invalid
-        // or absent blocks) become 0, so that no NaN pattern of an unwritten slot reaches the MFMA.
+        for (int nt = 0; nt < NT; ++nt) {
+          float p[8];
+          uint32_t pw[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int t0 = (jg0 + u) * kBlock + 4 * g;
-          const int nv = (2 * s2 + u < wn && x.pb[u] >= 0) ? min(max(T - t0, 0), 4) : 0;
-          if (nv < 4) {
-            const uint32_t mask = (1u << (8 * nv)) - 1u;
+          for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][i], kExpCoef, nml[nt])) * invl[nt];
 #pragma unroll
-            for (int dtl = 0; dtl < DTW; ++dtl) x.v[u][dtl] &= mask;
-            x.sc[u].x = nv > 0 ? x.sc[u].x : 0.0f;
-            x.sc[u].y = nv > 1 ? x.sc[u].y : 0.0f;
-            x.sc[u].z = nv > 2 ? x.sc[u].z : 0.0f;
-            x.sc[u].w = nv > 3 ? x.sc[u].w : 0.0f;
-          }
+          for (int w = 0; w < 4; ++w) pw[w] = pack_bf16x2(p[2 * w], p[2 * w + 1]);
+          pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
         }
-        uint4 (*lvb)[64] = lv[s2 & 1];
 #pragma unroll
-        for (int dtl = 0; dtl < DTW; ++dtl) {
-          const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dtl], false);
-          const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[0][dtl], true);
-          const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dtl], false);
-          const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(x.v[1][dtl], true);
-          lvb[wave * DTW + dtl][lane] =
-              make_uint4(pack_bf16x2(f01.x * x.sc[0].x, f01.y * x.sc[0].y), pack_bf16x2(f23.x * x.sc[0].z, f23.y * x.sc[0].w),
-                         pack_bf16x2(f45.x * x.sc[1].x, f45.y * x.sc[1].y), pack_bf16x2(f67.x * x.sc[1].z, f67.y * x.sc[1].w));
-        }
-        if constexpr (RING == 1) {
-          // The stage's registers are dead now (K multiplied, V codes and scales in LDS): the
-          // next stage's loads go out here, and the barrier waits for LDS only, so they stay in
-          // flight under it and under this stage's p.V products.
-          load_stage(s2 + 1, x);
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-          __builtin_amdgcn_s_barrier();
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        } else {
-          __syncthreads();
-        }
-        // every wavefront's tiles are in LDS; the other buffer is free again (its readers passed
-        // this barrier after their own reads of the previous stage)
-        if (mine) {
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const bf16x8 vop = __builtin_bit_cast(bf16x8, lvb[dt][lane]);
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[nt], acc[dt][nt], 0, 0, 0);
-          }
-        }
+          for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.vh[dt], pop[nt], acc[dt][nt], 0, 0, 0);
+        load_vh(s2 + 1, x);
       }
     };
     // RING stages in flight: one exit, at the loop head, and unconditional reloads (a break
     // between the stages would make the compiler wait for every load at the head; a reload
-    // past the window reads block 0 and is not computed).  Pass 2 runs every stage of the
-    // workgroup's window in every wavefront (each dequantizes its share of the V operand, with
-    // a barrier per stage); pass 1 only this wavefront's blocks.
-    const int nst = OUT ? ((wn + 1) >> 1) : ((jn + 1) >> 1);
+    // past the window reads page 0 and is not computed).  Each wavefront runs the stages of
+    // its own blocks; no wavefront waits for another.
+    const int nst = (jn + 1) >> 1;
     Stage ring[RING];
 #pragma unroll
-    for (int i = 0; i < RING; ++i) load_stage(i, ring[i]);
+    for (int i = 0; i < RING; ++i) {
+      load_k(i, ring[i]);
+      if constexpr (OUT) load_vh(i, ring[i]);
+    }
     for (int s2 = 0; s2 < nst; s2 += RING) {
 #pragma unroll
       for (int i = 0; i < RING; ++i) {
         const int ss = s2 + i;
-        if (ss < nst) compute_stage(ss, ring[i]);  // workgroup-uniform in pass 2, wave-uniform in pass 1
-        if (!OUT || RING > 1 || ss >= nst) load_stage(ss + RING, ring[i]);  // else done inside
+        if (ss < nst) compute_stage(ss, ring[i]);  // wave-uniform
+        if (!OUT) load_k(ss + RING, ring[i]);     // pass 2 loads inside the stage
+      }
+    }
+  }
+
+  if constexpr (!OUT) {
+    // Pass 2's V operand: stage sg of the group (blocks 2sg, 2sg+1) is dequantized by this
+    // launch's workgroup sg mod gridDim.x, one dimension tile group per wavefront, as
+    // bf16(fp32(code) * scale).  Codes and scales of tokens that are not in the sequence (past
+    // T, invalid or absent blocks) become 0, so that no NaN pattern of an unwritten slot reaches
+    // the MFMA.
+    const int nbk = (T + kBlock - 1) / kBlock;
+    for (int sg = (int)blockIdx.x; sg < (nbk + 1) >> 1; sg += (int)gridDim.x) {
+      uint32_t w[2][DTW];
+      float4 sc[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int jb = 2 * sg + u;
+        int pb = jb < nbk ? btrow[jb] : -1;
+        pb = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
+        const int64_t pg = max(pb, 0);
+        const uint8_t* vp = vlayer + pg * kpage;
+#pragma unroll
+        for (int dtl = 0; dtl < DTW; ++dtl) w[u][dtl] = *reinterpret_cast<const uint32_t*>(vp + (voff + dtl * 16u * kBlock));
+        sc[u] = *reinterpret_cast<const float4*>(slayer + pg * spage + 4 * g);
+        const int t0 = jb * kBlock + 4 * g;
+        const int nv = pb >= 0 ? min(max(T - t0, 0), 4) : 0;
+        const uint32_t mask = nv >= 4 ? 0xFFFFFFFFu : (1u << (8 * nv)) - 1u;
+#pragma unroll
+        for (int dtl = 0; dtl < DTW; ++dtl) w[u][dtl] &= mask;
+        sc[u].x = nv > 0 ? sc[u].x : 0.0f;
+        sc[u].y = nv > 1 ? sc[u].y : 0.0f;
+        sc[u].z = nv > 2 ? sc[u].z : 0.0f;
+        sc[u].w = nv > 3 ? sc[u].w : 0.0f;
+      }
+      uint4* dst = a.vhat + ((int64_t)grp * a.vh_stages + sg) * (DT * 64) + lane;
+#pragma unroll
+      for (int dtl = 0; dtl < DTW; ++dtl) {
+        const f32x2 f01 = __builtin_amdgcn_cvt_pk_f32_fp8(w[0][dtl], false);
+        const f32x2 f23 = __builtin_amdgcn_cvt_pk_f32_fp8(w[0][dtl], true);
+        const f32x2 f45 = __builtin_amdgcn_cvt_pk_f32_fp8(w[1][dtl], false);
+        const f32x2 f67 = __builtin_amdgcn_cvt_pk_f32_fp8(w[1][dtl], true);
+        dst[(wave * DTW + dtl) * 64] =
+            make_uint4(pack_bf16x2(f01.x * sc[0].x, f01.y * sc[0].y), pack_bf16x2(f23.x * sc[0].z, f23.y * sc[0].w),
+                       pack_bf16x2(f45.x * sc[1].x, f45.y * sc[1].y), pack_bf16x2(f67.x * sc[1].z, f67.y * sc[1].w));
       }
     }
   }
@@ -2056,11 +2105,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       float m = m_run[nt], l = l_run[nt];
       merge_lanes<16>(m, l);
       merge_lanes<32>(m, l);
-      if (g == 0 && rv[nt]) st[(int64_t)(row0 + nt * 16 + n) * kPrefillSplit + split] = make_float2(m, l);
+      if (g == 0 && rv[nt]) st[(int64_t)(row0 + nt * 16 + n) * a.pf_split + split] = make_float2(m, l);
     }
   } else {
     // lane (g, n) holds O^T[dims dt*16 + 4g .. +3][row nt*16 + n] of this part's keys
-    static_assert(NT == 1, "the part slots hold one row tile per wavefront");
     bool write = true;
     if (nparts > 1) {  // workgroup-uniform
       // Every part writes its fp32 partial to its slot (device-scope stores), waits for them,
@@ -2068,16 +2116,19 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       // area, read as 0 when it carries another call's tag.  The part that completes the count
       // sums the slots in part order (its own from registers), writes the output and zeroes the
       // counter.  Nobody waits for anybody: the order of arrival changes who sums, not the sum.
-      const int nrg = (a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves);
-      const int64_t slot_f = (int64_t)kPrefillRows * kPrefillWaves * D;  // floats per part slot
-      float* slots = a.partial + ((int64_t)grp * nrg + rgi) * nparts * slot_f;
-      const int rl = wave * kPrefillRows + n;  // row within the row group
+      const int nrg = (a.R + kPass2Rows - 1) / kPass2Rows;
+      constexpr int slot_b = kPass2Rows * D * 4;  // bytes per part slot
+      // the row group's slots, written and read with 16-byte device-scope (sc1) accesses
+      const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+          a.partial + ((int64_t)grp * nrg + rgi) * nparts * (slot_b / 4), (short)0, nparts * slot_b, 0x00020000);
+      // lane (g, n): row wave*ROWS + nt*16 + n, dimensions dt*16 + 4g .. +3
+      const int lofs = ((wave * ROWS + n) * D + 4 * g) * 4;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __hip_atomic_store(slots + split * slot_f + (int64_t)rl * D + dt * 16 + 4 * g + i, acc[dt][0][i],
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int dt = 0; dt < DT; ++dt)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[dt][nt]), srs,
+                                                 split * slot_b + lofs + (nt * 16 * D + dt * 16) * 4, 0, 16);
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       SDV_VMCNT0();
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -2105,23 +2156,36 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
       __syncthreads();
       write = s_last;
       if (write) {
+        // the parts' sum in part order, each part's slot loaded whole before it is added
+        f32x4 sum[DT][NT];
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          f32x4 sum = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-          for (int k = 0; k < nparts; ++k) {
-            f32x4 v;
-            if (k == split) {
-              v = acc[dt][0];
-            } else {
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
-                v[i] = __hip_atomic_load(slots + k * slot_f + (int64_t)rl * D + dt * 16 + 4 * g + i, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            }
-            sum += v;
+          for (int dt = 0; dt < DT; ++dt) sum[dt][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int k = 0; k < nparts; ++k) {  // workgroup-uniform
+          f32x4 v[DT][NT];
+          if (k == split) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+              for (int dt = 0; dt < DT; ++dt) v[dt][nt] = acc[dt][nt];
+          } else {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+              for (int dt = 0; dt < DT; ++dt)
+                v[dt][nt] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, k * slot_b + lofs + (nt * 16 * D + dt * 16) * 4, 0, 16));
           }
-          acc[dt][0] = sum;
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) sum[dt][nt] += v[dt][nt];
         }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) acc[dt][nt] = sum[dt][nt];
       }
     }
     if (write) {
@@ -2398,6 +2462,9 @@ struct Plan {
   bool group;                                     // group_kernel serves the call (many one-tile groups)
   int tpad;                                       // group_kernel: scratch row length (tokens)
   int pf_parts;                                   // prefill pass 2: key parts per row group
+  int pf_split;                                   // prefill pass 1: key parts per row group
+  size_t off_vhat;                                // prefill: dequantized V (pass 1 -> pass 2)
+  int vh_stages;                                  // prefill: two-block stages per group
   size_t total;                                   // bytes for every layout the call may take
 };
 
@@ -2438,19 +2505,31 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->group = false;
   p->tpad = 0;
   p->pf_parts = 1;
+  p->pf_split = 1;
+  p->off_vhat = 0;
+  p->vh_stages = 0;
   if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) of each key part
     p->off_scores = kSyncBytes;
     p->off_stats = kSyncBytes;
-    const size_t stats = round_up((size_t)(groups * R * 8 * kPrefillSplit), 256);
+    const int nbk = (max_seq_len + kBlock - 1) / kBlock;
+    const int max_parts = min(kPrefillMaxParts, max(1, nbk / 8));
+    const int64_t nrg1 = (R + kPass1Tiles * kPrefillRows * kPrefillWaves - 1) / (kPass1Tiles * kPrefillRows * kPrefillWaves);
+    p->pf_split = (int)std::max<int64_t>(1, std::min<int64_t>(max_parts, pass1_workgroups(D) / (groups * nrg1)));
+    const size_t stats = round_up((size_t)(groups * R * 8 * p->pf_split), 256);
     p->off_partial = p->off_stats + stats;
     // pass 2 splits the keys too when its counters (one per row group) fit the sync area's
     // statistics region; its part slots follow the statistics
-    const int64_t nrg = (R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves);
-    p->pf_parts = (prefill_parts(D) > 1 && groups * nrg <= (int64_t)(kSyncStatsBytes / 8)) ? prefill_parts(D) : 1;
+    const int64_t nrg = (R + kPass2Rows - 1) / kPass2Rows;
+    p->pf_parts = groups * nrg <= (int64_t)(kSyncStatsBytes / 8)
+                      ? (int)std::max<int64_t>(1, std::min<int64_t>(std::min(max_parts, kPrefillMaxParts2), pass2_workgroups(D) / (groups * nrg)))
+                      : 1;
     const size_t parts = p->pf_parts > 1
-                             ? round_up((size_t)(groups * nrg * p->pf_parts * kPrefillRows * kPrefillWaves * D * 4), 256)
+                             ? round_up((size_t)(groups * nrg * p->pf_parts * kPass2Rows * D * 4), 256)
                              : 0;
-    p->total = p->off_partial + parts;
+    // pass 1 dequantizes V once for pass 2: D/16 x 1 KiB per stage of two blocks
+    p->vh_stages = (((max_seq_len + kBlock - 1) / kBlock) + 1) / 2;
+    p->off_vhat = p->off_partial + parts;
+    p->total = p->off_vhat + (size_t)groups * p->vh_stages * (D / 16) * 1024;
     return true;
   }
   // the sync area [0, kSyncBytes) is shared by every layout and only the fused kernel uses it
@@ -2682,8 +2761,10 @@ template <int D>
 static bool launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t st, int phases) {
   if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
     if (a.app_v) return false;
-    const dim3 grid((unsigned)((a.R + kPrefillRows * kPrefillWaves - 1) / (kPrefillRows * kPrefillWaves)), a.KV, zdim);
-    const dim3 grid1(grid.x * kPrefillSplit, grid.y, grid.z), grid2(grid.x * a.pf_parts, grid.y, grid.z);
+    const dim3 grid((unsigned)((a.R + kPass2Rows - 1) / kPass2Rows), a.KV, zdim);
+    constexpr int rows1 = kPass1Tiles * 16 * kPrefillWaves;  // pass 1 rows per workgroup
+    const dim3 grid1((unsigned)((a.R + rows1 - 1) / rows1) * a.pf_split, grid.y, grid.z),
+        grid2(grid.x * a.pf_parts, grid.y, grid.z);
     if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPrefillWaves), 0, st, a);
     if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid2, dim3(64 * kPrefillWaves), 0, st, a);
     return true;
@@ -2830,6 +2911,9 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.n_pv_chunks = p.n_pv_chunks;
   a.score_stride = p.score_stride;
   a.pf_parts = p.pf_parts;
+  a.pf_split = p.pf_split;
+  a.vhat = reinterpret_cast<uint4*>(ws + p.off_vhat);
+  a.vh_stages = p.vh_stages;
   // RN(1/sqrt(D)): 1/sqrt(128) = 0.08838834764831845, 1/sqrt(64) = 0.125 exactly
   a.inv_sqrt_d = head_dim == 128 ? 0.08838834764831845f : 0.125f;
 

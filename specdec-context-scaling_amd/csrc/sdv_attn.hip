@@ -1750,13 +1750,15 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 //           V, each stage of two blocks once, as bf16(fp32(code) * scale) in the lane order of
 //           pass 2's MFMA operand.
 //   pass 2  merges the parts in part order into (M, L); each wavefront (32 rows) streams its
-//           part of the blocks again, two at a time, recomputes its rows' BF16 scores and forms
+//           part of the blocks again, recomputes its rows' BF16 scores and forms
 //           p = bf16(exp(s - M) / L) in registers.  A lane's S^T fragment (row n, tokens
-//           4g..4g+3 of each of the two blocks) is exactly the B operand of O^T = V_hat^T P^T
-//           with those 8 tokens as its k-slots; the A operand is the stage's dequantized V,
-//           16 bytes per lane and dimension tile, loaded like K.  No wavefront waits for
-//           another.  O^T accumulates in fp32; the parts' partials are summed in part order
-//           by the last part to finish, and leave as BF16, four dimensions of one row per lane.
+//           4g..4g+3 of each of two blocks) is exactly the B operand of O^T = V_hat^T P^T with
+//           those 8 tokens as its k-slots; the A operand is the dequantized V of the two
+//           blocks, 16 bytes per lane and dimension tile.  O^T accumulates in fp32; the parts'
+//           partials are summed in part order by the last part to finish, and leave as BF16,
+//           four dimensions of one row per lane.
+// Both passes stream stages of four blocks whose K (and dequantized V) the workgroup's four
+// wavefronts load once and share through LDS, one barrier per stage.
 // Rows are head-major (row r: head r / S, token r % S) as in the other kernels.  Row r sees
 // keys j <= T - S + r % S (the eager mask); T >= S is the caller's contract (the S new tokens
 // are part of the context), and a row that sees no key outputs 0.  The page ids of the
@@ -1764,12 +1766,13 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // 12/2/128 and 14/2/64, both passes): 451 / 324 us with 16 rows per wavefront and V dequantized
 // per stage into LDS by the workgroup; scalar branches for the unmasked stages 442 / 281;
 // two row tiles in pass 1 382 / 263; two in pass 2 350 / 235; V dequantized by pass 1 and
-// MFMA results in VGPRs 332 / 218; 16-byte part slots and key parts per launch size 303 / 196.
+// MFMA results in VGPRs 332 / 218; 16-byte part slots and key parts per launch size 303 / 196;
+// each stage's K and V loaded once per workgroup and shared through LDS 284 / 182; stages of
+// four blocks, products issued by phase 271 / 173.
 constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
 constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
-// pass 1: stages (two blocks each) in flight per wavefront (3 measured equal, 4 slower)
-constexpr int kPrefillRing = 2;
-constexpr int kPrefillWindow = 2048;  // page ids staged in LDS per round
+constexpr int kPrefillWindow = 1024;  // page ids staged in LDS per round
+constexpr int kStageBlocks = 4;      // page blocks per stage (a multiple of 2 dividing the window)
 // Pass 1: row tiles per wavefront (each K operand it loads serves this many tiles; 2048 x 8192,
 // pass 1 with one tile 158 / 93 us (12/2/128 / 14/2/64), with two 101 / 77 us)
 constexpr int kPass1Tiles = 2;
@@ -1860,7 +1863,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
   const int* btrow = a.block_table + (int64_t)b * a.max_blocks;
   float2* st = a.stats + (int64_t)grp * a.R * a.pf_split;  // row r, pass-1 part k: st[r * a.pf_split + k]
   // this workgroup's key blocks: part `split` of [0, nblk_wg)
-  const int part = (((nblk_wg + nparts - 1) / nparts) + 1) & ~1;  // even: whole stages
+  const int part = (((nblk_wg + nparts - 1) / nparts) + kStageBlocks - 1) & ~(kStageBlocks - 1);  // whole stages
   const int blo = min(nblk_wg, split * part);
   const int bhi = min(nblk_wg, blo + part);
 
@@ -1910,147 +1913,160 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
     for (int dt = 0; dt < DT; ++dt) acc[dt][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  // A stage is two consecutive blocks u = 0, 1: their page ids and K operands and, for pass 2,
-  // the stage's dequantized V operand (D/16 tiles, written by pass 1).  Pass 1 keeps
-  // kPrefillRing stages in flight; pass 2 keeps one, and loads the next stage's K as soon as
-  // the stage's q.k^T products are issued and its V operand after the p.V products.
-  constexpr int RING = OUT ? 1 : kPrefillRing;
-  struct Stage {
-    bf16x8 k[2][KK];
-    bf16x8 vh[OUT ? DT : 1];
-    int pb[2];
-  };
+  // A stage is kStageBlocks = 4 consecutive blocks u = 0..3.  Its K operands (4 x KK chunks of
+  // 1 KiB: block u, 32-dimension slice kk, in the lane order of the MFMA's A operand) and, for
+  // pass 2, its dequantized V operand (2 x DT chunks of 1 KiB: pair h of blocks, dimension tile
+  // dt, written by pass 1) are the same for every row, so the workgroup loads each chunk once
+  // and shares it through LDS: wavefront w loads chunks w, w + W, ... of stage s + 1 into
+  // registers while the workgroup computes stage s, and writes them to the other LDS buffer
+  // after the next barrier.  One barrier per stage publishes the stage and frees the other
+  // buffer.  Within a stage the q.k^T products of all four blocks go out first, then the
+  // scores, then the p.V products: the MFMA unit has independent work while the VALU rounds.
+  constexpr int W = kPrefillWaves, SB = kStageBlocks;
+  constexpr int NKC = SB * KK, NC = NKC + (OUT ? (SB / 2) * DT : 0), CPW = NC / W;
+  static_assert(CPW * W == NC && NKC % W == 0, "the wavefronts share the chunks evenly");
+  __shared__ uint4 ring[2][NC * 64];
   const uint4* vh_grp = a.vhat + (int64_t)grp * a.vh_stages * (DT * 64) + lane;
   for (int w0 = blo; w0 < bhi; w0 += kPrefillWindow) {  // workgroup-uniform
     const int wn = min(kPrefillWindow, bhi - w0);
     __syncthreads();  // the previous window's page ids are no longer read
-    for (int j = tid; j < wn; j += 64 * kPrefillWaves) {
+    for (int j = tid; j < wn; j += 64 * W) {
       const int pb = btrow[w0 + j];
       lpb[j] = (pb >= 0 && pb < a.num_blocks) ? pb : -1;
     }
     __syncthreads();
     const int jn = max(0, min(nblk - w0, wn));  // this wavefront's blocks in the window
-    // a block past jn (or invalid) reads page 0, which is always allocated; it is never used
-    auto load_k = [&](int s2, Stage& x) {
+    const int nst = (wn + SB - 1) / SB;         // the workgroup's stages in the window
+    // page id of block jb of the window (jb < wn; the same word in every lane)
+    auto page = [&](int jb) { return __builtin_amdgcn_readfirstlane(lpb[jb]); };
+    uint4 stg[CPW];  // this wavefront's chunks of the next stage
+    auto fetch = [&](int s4) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int jb = 2 * s2 + u;
-        int pb = -1;
-        if (jb < jn) pb = __builtin_amdgcn_readfirstlane(lpb[jb]);  // the same word in every lane
-        x.pb[u] = pb;
-        const int64_t pg = max(pb, 0);
-        const uint16_t* kp = klayer + pg * kpage;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) x.k[u][kk] = __builtin_bit_cast(bf16x8, load_stream16(kp + (koff + kk * 512u)));
+      for (int j = 0; j < CPW; ++j) {
+        const int c = j * W + wave;
+        if (j < NKC / W) {  // a K chunk: block u, slice kk; past the window, page 0 (never used)
+          const int u = c / KK, kk = c - u * KK;
+          const int jb = SB * s4 + u;
+          const int pb = __builtin_amdgcn_readfirstlane(lpb[min(jb, kPrefillWindow - 1)]);
+          const int64_t pg = jb < wn ? max(pb, 0) : 0;
+          stg[j] = load_stream16(klayer + pg * kpage + (koff + kk * 512u));
+        } else {            // a dequantized V chunk: pair h, dimension tile dt
+          const int h = (c - NKC) / DT, dt = (c - NKC) - h * DT;
+          const int sg = min((w0 >> 1) + (SB / 2) * s4 + h, a.vh_stages - 1);
+          stg[j] = vh_grp[(int64_t)sg * (DT * 64) + dt * 64];
+        }
       }
     };
-    // the stage's V operand; a stage past the group's (a reload after the last stage) reads
-    // the last one and is not used
-    auto load_vh = [&](int s2, Stage& x) {
-      const int sg = min((w0 >> 1) + s2, a.vh_stages - 1);
-      const uint4* src = vh_grp + (int64_t)sg * (DT * 64);
+    auto stash = [&](int s4) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) x.vh[dt] = __builtin_bit_cast(bf16x8, src[dt * 64]);
+      for (int j = 0; j < CPW; ++j) ring[s4 & 1][(j * W + wave) * 64 + lane] = stg[j];
     };
-    auto qk = [&](const Stage& x, int u, int nt) {
-      f32x4 s = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute_stage = [&](int s4, const uint4* sb) {
+      const int jb0 = SB * s4, jg0 = w0 + jb0;  // window and global block of u = 0
+      int pb[SB];
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.k[u][kk], qop[nt][kk], s, 0, 0, 0);
-      return s;
-    };
-    auto compute_stage = [&](int s2, Stage& x) {
-      const int jg0 = w0 + 2 * s2;  // global block of u = 0
+      for (int u = 0; u < SB; ++u) pb[u] = jb0 + u < jn ? page(jb0 + u) : -1;
       // scalar: every key of the stage exists, is valid and is seen by every row
-      const bool full = jg0 + 2 <= nfull && 2 * s2 + 1 < jn && x.pb[0] >= 0 && x.pb[1] >= 0;
-      float y[NT][8];  // the stage's scores (in units of kUnit), u = 0 in 0-3, u = 1 in 4-7
-      if (full) {
+      bool full = jg0 + SB <= nfull && jb0 + SB <= jn;
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < SB; ++u) full = full && pb[u] >= 0;
+      // q.k^T of the stage's blocks, all issued before any score is rounded
+      f32x4 sacc[SB][NT];
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) eager4(qk(x, u, nt), y[nt] + 4 * u);
-      } else {
+      for (int u = 0; u < SB; ++u)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          if (2 * s2 + u < jn) {  // scalar
-            const int t0 = (jg0 + u) * kBlock + 4 * g;
-            const bool blk_ok = x.pb[u] >= 0;
+        for (int nt = 0; nt < NT; ++nt) sacc[u][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              eager4(qk(x, u, nt), y[nt] + 4 * u);
+      for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-              for (int i = 0; i < 4; ++i) y[nt][4 * u + i] = (blk_ok && t0 + i <= lim[nt]) ? y[nt][4 * u + i] : -INFINITY;
-            }
-          } else {
+        for (int u = 0; u < SB; ++u) {
+          const bf16x8 kop = __builtin_bit_cast(bf16x8, sb[(u * KK + kk) * 64 + lane]);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+          for (int nt = 0; nt < NT; ++nt) sacc[u][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[nt][kk], sacc[u][nt], 0, 0, 0);
+        }
+      float y[NT][4 * SB];  // the stage's scores (in units of kUnit): block u in 4u .. 4u+3
 #pragma unroll
-              for (int i = 0; i < 4; ++i) y[nt][4 * u + i] = -INFINITY;
-          }
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) eager4(sacc[u][nt], y[nt] + 4 * u);
+      if (!full) {
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int t0 = (jg0 + u) * kBlock + 4 * g;
+          const bool blk_ok = pb[u] >= 0;  // -1 also for a block past this wavefront's
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[nt][4 * u + i] = (blk_ok && t0 + i <= lim[nt]) ? y[nt][4 * u + i] : -INFINITY;
         }
       }
       if constexpr (!OUT) {
-        // Online (max, sum) per lane, one update per stage: the max of the stage's eight scores
-        // first, then the running sum rescaled once by exp2((m_old - m_new) log2 e), which is
-        // exactly 1 while the max stays (the one-FMA form exp2(m_old log2 e - RN(m_new log2 e))
-        // is off by the product's rounding on every update, and L drifted by ~1e-5 at T = 8192:
-        // rel-L2 7e-4 against eager).  A lane sums at most T/32 terms of at most 1 each, so the
-        // plain fp32 sum is within ~1e-5 relative of the exact one.  A stage without masked keys
-        // has a finite max, and exp2(-inf) = 0 covers the first update.
+        // Online (max, sum) per lane, one update per stage: the max of the stage's scores first,
+        // then the running sum rescaled once by exp2((m_old - m_new) log2 e), which is exactly 1
+        // while the max stays (the one-FMA form exp2(m_old log2 e - RN(m_new log2 e)) is off by
+        // the product's rounding on every update, and L drifted by ~1e-5 at T = 8192: rel-L2
+        // 7e-4 against eager).  A lane sums at most T/32 terms of at most 1 each, so the plain
+        // fp32 sum is within ~1e-5 relative of the exact one.  A stage without masked keys has
+        // a finite max, and exp2(-inf) = 0 covers the first update.
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const float* yt = y[nt];
-          const float mt =
-              fmaxf(fmaxf(fmaxf(yt[0], yt[1]), fmaxf(yt[2], yt[3])), fmaxf(fmaxf(yt[4], yt[5]), fmaxf(yt[6], yt[7]))) * kUnit;
+          float mr[SB];
+#pragma unroll
+          for (int u = 0; u < SB; ++u) mr[u] = fmaxf(fmaxf(yt[4 * u], yt[4 * u + 1]), fmaxf(yt[4 * u + 2], yt[4 * u + 3]));
+          const float mt = fmaxf(fmaxf(mr[0], mr[1]), fmaxf(mr[2], mr[3])) * kUnit;
           if (full || mt != -INFINITY) {
 #pragma clang fp contract(off)
             const float mn = fmaxf(m_run[nt], mt), nm = -mn * kLog2e;
             const float f = __builtin_amdgcn_exp2f((m_run[nt] - mn) * kLog2e);
-            float e[8];
+            float e[4 * SB];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(yt[i], kExpCoef, nm));
-            const float xs = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
-            l_run[nt] = l_run[nt] * f + xs;
+            for (int i = 0; i < 4 * SB; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(yt[i], kExpCoef, nm));
+            float xs[SB];
+#pragma unroll
+            for (int u = 0; u < SB; ++u) xs[u] = (e[4 * u] + e[4 * u + 1]) + (e[4 * u + 2] + e[4 * u + 3]);
+            l_run[nt] = l_run[nt] * f + ((xs[0] + xs[1]) + (xs[2] + xs[3]));
             m_run[nt] = mn;
           }
         }
       } else {
-        load_k(s2 + 1, x);  // the K registers are free once the products are issued
-        bf16x8 pop[NT];     // packed BF16 probabilities: u = 0 in elements 0-3, u = 1 in 4-7
+        // p for each pair h of blocks: the B operand of one p.V product (tokens 4g..4g+3 of the
+        // pair's first block, then of its second)
+        bf16x8 pop[SB / 2][NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          float p[8];
-          uint32_t pw[4];
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][i], kExpCoef, nml[nt])) * invl[nt];
+          for (int h = 0; h < SB / 2; ++h) {
+            uint32_t pw[4];
 #pragma unroll
-          for (int w = 0; w < 4; ++w) pw[w] = pack_bf16x2(p[2 * w], p[2 * w + 1]);
-          pop[nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        }
+            for (int w = 0; w < 4; ++w) {
+              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][8 * h + 2 * w], kExpCoef, nml[nt])) * invl[nt];
+              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][8 * h + 2 * w + 1], kExpCoef, nml[nt])) * invl[nt];
+              pw[w] = pack_bf16x2(p0, p1);
+            }
+            pop[h][nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+          }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x.vh[dt], pop[nt], acc[dt][nt], 0, 0, 0);
-        load_vh(s2 + 1, x);
+          for (int h = 0; h < SB / 2; ++h) {
+            const bf16x8 vop = __builtin_bit_cast(bf16x8, sb[(NKC + h * DT + dt) * 64 + lane]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[h][nt], acc[dt][nt], 0, 0, 0);
+          }
       }
     };
-    // RING stages in flight: one exit, at the loop head, and unconditional reloads (a break
-    // between the stages would make the compiler wait for every load at the head; a reload
-    // past the window reads page 0 and is not computed).  Each wavefront runs the stages of
-    // its own blocks; no wavefront waits for another.
-    const int nst = (jn + 1) >> 1;
-    Stage ring[RING];
-#pragma unroll
-    for (int i = 0; i < RING; ++i) {
-      load_k(i, ring[i]);
-      if constexpr (OUT) load_vh(i, ring[i]);
-    }
-    for (int s2 = 0; s2 < nst; s2 += RING) {
-#pragma unroll
-      for (int i = 0; i < RING; ++i) {
-        const int ss = s2 + i;
-        if (ss < nst) compute_stage(ss, ring[i]);  // wave-uniform
-        if (!OUT) load_k(ss + RING, ring[i]);     // pass 2 loads inside the stage
-      }
+    fetch(0);
+    stash(0);
+    fetch(1);
+    for (int ss = 0; ss < nst; ++ss) {  // workgroup-uniform
+      // stage ss is in LDS for every wavefront, and every wavefront is done with stage ss - 1
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      stash(ss + 1);  // into the buffer of stage ss - 1
+      fetch(ss + 2);
+      if (SB * ss < jn) compute_stage(ss, ring[ss & 1]);  // scalar: the stage has keys this wavefront's rows see
     }
   }
 

@@ -103,6 +103,16 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
 
 __device__ __forceinline__ bf16x8 zero_bf16x8() { return __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0)); }
 
+// max of three fp32 values in one instruction (v_max3_f32).  fmaxf on values the compiler
+// cannot prove canonical (scores unpacked from BF16 bit patterns) costs a canonicalising
+// v_max per operand first; the scores here are never signalling NaNs, so the plain instruction
+// gives fmaxf's result.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ int seq_len_of(const AttnArgs& a, int b) {
   return a.seq_lens ? min(max(a.seq_lens[b], 0), a.max_seq_len) : a.max_seq_len;
 }
@@ -1768,7 +1778,8 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // two row tiles in pass 1 382 / 263; two in pass 2 350 / 235; V dequantized by pass 1 and
 // MFMA results in VGPRs 332 / 218; 16-byte part slots and key parts per launch size 303 / 196;
 // each stage's K and V loaded once per workgroup and shared through LDS 284 / 182; stages of
-// four blocks, products issued by phase 271 / 173.
+// four blocks, products issued by phase 271 / 173; v_max3 for the stage max and register
+// budgets held per pass 265 / 171.
 constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
 constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
 constexpr int kPrefillWindow = 1024;  // page ids staged in LDS per round
@@ -1793,8 +1804,13 @@ constexpr int kPrefillMaxParts = 64;
 // pass 2: the last part to finish adds every part's slot of its row group
 constexpr int kPrefillMaxParts2 = 8;
 
+// Resident wavefronts per SIMD the register budget is held to: pass 1 four (at most 128
+// VGPRs), pass 2 three for head_dim 64 (168) and two for 128 (its 64 fp32 accumulators per lane).
+constexpr int prefill_waves_per_simd(int D, bool OUT) { return !OUT ? 4 : D == 64 ? 3 : 2; }
+
 template <int D, bool OUT>
-__global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, OUT))))
+void prefill_kernel(AttnArgs a) {
   // row tiles of 16 rows per wavefront: two in pass 1 (each K operand serves 32 rows), one in
   // pass 2
   constexpr int KK = D / 32, DT = D / 16, NT = OUT ? kPass2Tiles : kPass1Tiles, ROWS = NT * 16;
@@ -2011,10 +2027,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void prefill_kernel(AttnArgs a)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const float* yt = y[nt];
-          float mr[SB];
-#pragma unroll
-          for (int u = 0; u < SB; ++u) mr[u] = fmaxf(fmaxf(yt[4 * u], yt[4 * u + 1]), fmaxf(yt[4 * u + 2], yt[4 * u + 3]));
-          const float mt = fmaxf(fmaxf(mr[0], mr[1]), fmaxf(mr[2], mr[3])) * kUnit;
+          static_assert(SB == 4, "the max below covers 16 scores");
+          const float m0 = max3f(yt[0], yt[1], yt[2]), m1 = max3f(yt[3], yt[4], yt[5]), m2 = max3f(yt[6], yt[7], yt[8]);
+          const float m3 = max3f(yt[9], yt[10], yt[11]), m4 = max3f(yt[12], yt[13], yt[14]);
+          const float mt = max3f(max3f(m0, m1, m2), max3f(m3, m4, yt[15]), -INFINITY) * kUnit;
           if (full || mt != -INFINITY) {
 #pragma clang fp contract(off)
             const float mn = fmaxf(m_run[nt], mt), nm = -mn * kLog2e;

@@ -1779,7 +1779,8 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // MFMA results in VGPRs 332 / 218; 16-byte part slots and key parts per launch size 303 / 196;
 // each stage's K and V loaded once per workgroup and shared through LDS 284 / 182; stages of
 // four blocks, products issued by phase 271 / 173; v_max3 for the stage max and register
-// budgets held per pass 265 / 171.
+// budgets held per pass 265 / 171; constant block indices in the loads and 1/L folded into
+// the exponent 258 / 167 (worst rel-L2 per 64-row block against eager 1.8e-4 -> 2.3e-4).
 constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
 constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
 constexpr int kPrefillWindow = 1024;  // page ids staged in LDS per round
@@ -1907,22 +1908,22 @@ void prefill_kernel(AttnArgs a) {
   };
 
   float m_run[NT], l_run[NT];   // pass 1: running max and sum
-  float nml[NT], invl[NT];      // pass 2: -M log2 e and 1/L per row
+  float nml[NT];                // pass 2: -M log2 e - log2 L per row
   f32x4 acc[DT][NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     m_run[nt] = -INFINITY;
     l_run[nt] = 0.0f;
     nml[nt] = 0.0f;
-    invl[nt] = 0.0f;
     if (OUT && rv[nt]) {
       // (M, L) of the row: its parts merged in part order
       const float2* sr = st + (int64_t)(row0 + nt * 16 + n) * a.pf_split;
       float m = sr[0].x, l = sr[0].y;
       for (int k = 1; k < a.pf_split; ++k) merge_fast(m, l, sr[k].x, sr[k].y);
       if (l > 0.0f) {
-        nml[nt] = -m * kLog2e;
-        invl[nt] = 1.0f / l;
+        // p = exp(s - M) / L as one exp2: 2^(s log2 e - M log2 e - log2 L) (v_log_f32 is within
+        // 1 ulp; |log2 L| <= log2 T, so p moves by ~1e-6 relative, far below its BF16 step)
+        nml[nt] = -m * kLog2e - __builtin_amdgcn_logf(l);
       }
     }
 #pragma unroll
@@ -1961,13 +1962,14 @@ void prefill_kernel(AttnArgs a) {
       for (int j = 0; j < CPW; ++j) {
         const int c = j * W + wave;
         if (j < NKC / W) {  // a K chunk: block u, slice kk; past the window, page 0 (never used)
-          const int u = c / KK, kk = c - u * KK;
+          // u is a constant when every wavefront's chunk j falls in the same block
+          const int u = KK % W == 0 ? (j * W) / KK : c / KK, kk = c - u * KK;
           const int jb = SB * s4 + u;
           const int pb = __builtin_amdgcn_readfirstlane(lpb[min(jb, kPrefillWindow - 1)]);
           const int64_t pg = jb < wn ? max(pb, 0) : 0;
           stg[j] = load_stream16(klayer + pg * kpage + (koff + kk * 512u));
         } else {            // a dequantized V chunk: pair h, dimension tile dt
-          const int h = (c - NKC) / DT, dt = (c - NKC) - h * DT;
+          const int h = DT % W == 0 ? (j * W - NKC) / DT : (c - NKC) / DT, dt = (c - NKC) - h * DT;
           const int sg = min((w0 >> 1) + (SB / 2) * s4 + h, a.vh_stages - 1);
           stg[j] = vh_grp[(int64_t)sg * (DT * 64) + dt * 64];
         }
@@ -1989,16 +1991,13 @@ void prefill_kernel(AttnArgs a) {
       // q.k^T of the stage's blocks, all issued before any score is rounded
       f32x4 sacc[SB][NT];
 #pragma unroll
-      for (int u = 0; u < SB; ++u)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) sacc[u][nt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
       for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
           const bf16x8 kop = __builtin_bit_cast(bf16x8, sb[(u * KK + kk) * 64 + lane]);
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) sacc[u][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[nt][kk], sacc[u][nt], 0, 0, 0);
+          for (int nt = 0; nt < NT; ++nt)
+            sacc[u][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[nt][kk], kk == 0 ? (f32x4){0.0f, 0.0f, 0.0f, 0.0f} : sacc[u][nt], 0, 0, 0);
         }
       float y[NT][4 * SB];  // the stage's scores (in units of kUnit): block u in 4u .. 4u+3
 #pragma unroll
@@ -2056,8 +2055,8 @@ void prefill_kernel(AttnArgs a) {
             uint32_t pw[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][8 * h + 2 * w], kExpCoef, nml[nt])) * invl[nt];
-              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][8 * h + 2 * w + 1], kExpCoef, nml[nt])) * invl[nt];
+              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][8 * h + 2 * w], kExpCoef, nml[nt]));
+              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(y[nt][8 * h + 2 * w + 1], kExpCoef, nml[nt]));
               pw[w] = pack_bf16x2(p0, p1);
             }
             pop[h][nt] = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));

@@ -1780,7 +1780,8 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // each stage's K and V loaded once per workgroup and shared through LDS 284 / 182; stages of
 // four blocks, products issued by phase 271 / 173; v_max3 for the stage max and register
 // budgets held per pass 265 / 171; constant block indices in the loads and 1/L folded into
-// the exponent 258 / 167 (worst rel-L2 per 64-row block against eager 1.8e-4 -> 2.3e-4).
+// the exponent 258 / 167 (worst rel-L2 per 64-row block against eager 1.8e-4 -> 2.3e-4); pass
+// 2's statistics loads eight parts at a time 253 / 160.
 constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
 constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
 constexpr int kPrefillWindow = 1024;  // page ids staged in LDS per round
@@ -1918,8 +1919,22 @@ void prefill_kernel(AttnArgs a) {
     if (OUT && rv[nt]) {
       // (M, L) of the row: its parts merged in part order
       const float2* sr = st + (int64_t)(row0 + nt * 16 + n) * a.pf_split;
-      float m = sr[0].x, l = sr[0].y;
-      for (int k = 1; k < a.pf_split; ++k) merge_fast(m, l, sr[k].x, sr[k].y);
+      // eight parts' loads in flight at a time, merged in part order
+      float m = -INFINITY, l = 0.0f;
+      for (int k0 = 0; k0 < a.pf_split; k0 += 8) {
+        float2 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = k0 + i < a.pf_split ? sr[k0 + i] : make_float2(-INFINITY, 0.0f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (k0 + i == 0) {
+            m = v[0].x;
+            l = v[0].y;
+          } else {
+            merge_fast(m, l, v[i].x, v[i].y);
+          }
+        }
+      }
       if (l > 0.0f) {
         // p = exp(s - M) / L as one exp2: 2^(s log2 e - M log2 e - log2 L) (v_log_f32 is within
         // 1 ulp; |log2 L| <= log2 T, so p moves by ~1e-6 relative, far below its BF16 step)

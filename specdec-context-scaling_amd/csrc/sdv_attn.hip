@@ -1783,7 +1783,9 @@ __global__ void zero_kernel(uint32_t* p, size_t n) {
 // the exponent 258 / 167 (worst rel-L2 per 64-row block against eager 1.8e-4 -> 2.3e-4); pass
 // 2's statistics loads eight parts at a time 253 / 160.
 constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
-constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
+constexpr int kPass1Waves = 4;     // wavefronts per workgroup, pass 1
+constexpr int kPass2Waves = 4;     // and pass 2
+constexpr int prefill_waves(bool OUT) { return OUT ? kPass2Waves : kPass1Waves; }
 constexpr int kPrefillWindow = 1024;  // page ids staged in LDS per round
 constexpr int kStageBlocks = 4;      // page blocks per stage (a multiple of 2 dividing the window)
 // Pass 1: row tiles per wavefront (each K operand it loads serves this many tiles; 2048 x 8192,
@@ -1792,7 +1794,7 @@ constexpr int kPass1Tiles = 2;
 // Pass 2: row tiles per wavefront, and the rows of a workgroup (a row group: its part slots,
 // its counter)
 constexpr int kPass2Tiles = 2;
-constexpr int kPass2Rows = kPass2Tiles * kPrefillRows * kPrefillWaves;
+constexpr int kPass2Rows = kPass2Tiles * kPrefillRows * kPass2Waves;
 // Both passes split each row group's keys in parts, one workgroup each (pass 2 merges pass 1's
 // (max, sum) in part order; the last pass-2 part to finish sums the parts' outputs), as many
 // as bring the launch to about this many workgroups, at most kPrefillMaxParts and none under
@@ -1811,13 +1813,14 @@ constexpr int kPrefillMaxParts2 = 8;
 constexpr int prefill_waves_per_simd(int D, bool OUT) { return !OUT ? 4 : D == 64 ? 3 : 2; }
 
 template <int D, bool OUT>
-__global__ __launch_bounds__(64 * kPrefillWaves) __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, OUT))))
+__global__ __launch_bounds__(64 * prefill_waves(OUT)) __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, OUT))))
 void prefill_kernel(AttnArgs a) {
   // row tiles of 16 rows per wavefront: two in pass 1 (each K operand serves 32 rows), one in
   // pass 2
   constexpr int KK = D / 32, DT = D / 16, NT = OUT ? kPass2Tiles : kPass1Tiles, ROWS = NT * 16;
-  constexpr int DTW = DT / kPrefillWaves;  // pass 1: dimension tiles of V each wavefront dequantizes
-  static_assert(DTW * kPrefillWaves == DT, "the wavefronts share the dimension tiles evenly");
+  constexpr int W = prefill_waves(OUT);
+  constexpr int DTW = DT / W;  // pass 1: dimension tiles of V each wavefront dequantizes
+  static_assert(OUT || DTW * W == DT, "the wavefronts share the dimension tiles evenly");
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   __shared__ int lpb[kPrefillWindow];
   __shared__ int s_kend;
@@ -1830,7 +1833,7 @@ void prefill_kernel(AttnArgs a) {
   const int nparts = OUT ? a.pf_parts : a.pf_split;
   const int split = (int)(blockIdx.x % nparts);
   const int rgi = (int)(blockIdx.x / nparts);
-  const int row0 = (rgi * kPrefillWaves + wave) * ROWS;
+  const int row0 = (rgi * W + wave) * ROWS;
 
   // this lane's rows (row tile nt: row row0 + nt*16 + n): q operand and last visible key
   bf16x8 qop[NT][KK];
@@ -1954,7 +1957,7 @@ void prefill_kernel(AttnArgs a) {
   // after the next barrier.  One barrier per stage publishes the stage and frees the other
   // buffer.  Within a stage the q.k^T products of all four blocks go out first, then the
   // scores, then the p.V products: the MFMA unit has independent work while the VALU rounds.
-  constexpr int W = kPrefillWaves, SB = kStageBlocks;
+  constexpr int SB = kStageBlocks;
   constexpr int NKC = SB * KK, NC = NKC + (OUT ? (SB / 2) * DT : 0), CPW = NC / W;
   static_assert(CPW * W == NC && NKC % W == 0, "the wavefronts share the chunks evenly");
   __shared__ uint4 ring[2][NC * 64];
@@ -2559,7 +2562,7 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
     p->off_stats = kSyncBytes;
     const int nbk = (max_seq_len + kBlock - 1) / kBlock;
     const int max_parts = min(kPrefillMaxParts, max(1, nbk / 8));
-    const int64_t nrg1 = (R + kPass1Tiles * kPrefillRows * kPrefillWaves - 1) / (kPass1Tiles * kPrefillRows * kPrefillWaves);
+    const int64_t nrg1 = (R + kPass1Tiles * kPrefillRows * kPass1Waves - 1) / (kPass1Tiles * kPrefillRows * kPass1Waves);
     p->pf_split = (int)std::max<int64_t>(1, std::min<int64_t>(max_parts, pass1_workgroups(D) / (groups * nrg1)));
     const size_t stats = round_up((size_t)(groups * R * 8 * p->pf_split), 256);
     p->off_partial = p->off_stats + stats;
@@ -2808,11 +2811,11 @@ static bool launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t s
   if (p.n_row_groups > 1) {  // many query rows: the two prefill passes
     if (a.app_v) return false;
     const dim3 grid((unsigned)((a.R + kPass2Rows - 1) / kPass2Rows), a.KV, zdim);
-    constexpr int rows1 = kPass1Tiles * 16 * kPrefillWaves;  // pass 1 rows per workgroup
+    constexpr int rows1 = kPass1Tiles * 16 * kPass1Waves;  // pass 1 rows per workgroup
     const dim3 grid1((unsigned)((a.R + rows1 - 1) / rows1) * a.pf_split, grid.y, grid.z),
         grid2(grid.x * a.pf_parts, grid.y, grid.z);
-    if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPrefillWaves), 0, st, a);
-    if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid2, dim3(64 * kPrefillWaves), 0, st, a);
+    if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPass1Waves), 0, st, a);
+    if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid2, dim3(64 * kPass2Waves), 0, st, a);
     return true;
   }
   if (phases == SDV_PHASE_ALL) {

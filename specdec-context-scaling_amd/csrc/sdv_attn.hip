@@ -1786,7 +1786,7 @@ constexpr int kPrefillRows = 16;   // query rows per MFMA row tile
 constexpr int kPass1Waves = 4;     // wavefronts per workgroup, pass 1
 constexpr int kPass2Waves = 4;     // and pass 2
 constexpr int prefill_waves(bool OUT) { return OUT ? kPass2Waves : kPass1Waves; }
-constexpr int kPrefillWindow = 1024;  // page ids staged in LDS per round
+constexpr int kPrefillWindow = 256;   // page ids staged in LDS per round
 constexpr int kStageBlocks = 4;      // page blocks per stage (a multiple of 2 dividing the window)
 // Pass 1: row tiles per wavefront (each K operand it loads serves this many tiles; 2048 x 8192,
 // pass 1 with one tile 158 / 93 us (12/2/128 / 14/2/64), with two 101 / 77 us)

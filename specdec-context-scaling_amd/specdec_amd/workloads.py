@@ -88,3 +88,45 @@ def bytes_quant_append(tokens: int, KV: int, D: int, with_k: bool) -> int:
     if with_k:
         per += KV * D * 2 * 2
     return tokens * per
+
+
+def prefill_chunk(q_heads: int, kv_heads: int, head_dim: int, rows: int, keys: int, seed: int = 901, device="cuda"):
+    """One layer's prefill chunk (f3): a paged cache of `keys` tokens (the chunk's `rows` new
+    tokens last) and q in the projection layout (1, rows, q_heads, head_dim).  Returns
+    (cache, q)."""
+    from .engine.paged_cache import PagedKVCache
+
+    g = gen(seed, device)
+    cache = PagedKVCache(kv_heads, head_dim, num_blocks=keys // 16 + 8, device=device, seed=seed + 1, growable=False)
+    cache.prefill(0, randn_bf16((keys, kv_heads, head_dim), g, device), randn_bf16((keys, kv_heads, head_dim), g, device),
+                  [keys])
+    return cache, randn_bf16((1, rows, q_heads, head_dim), g, device)
+
+
+def _main(argv=None) -> None:
+    """python -m specdec_amd.workloads prefill [--calls N]: the reference's prefill chunk (2048
+    query rows over 8192 keys) for the target (12/2/128) and the draft (14/2/64), N eager calls
+    each -- a fixed workload for rocprofv3 counter runs."""
+    import argparse
+
+    from .kernels import ops
+
+    ap = argparse.ArgumentParser(prog="python -m specdec_amd.workloads")
+    ap.add_argument("workload", choices=("prefill",))
+    ap.add_argument("--calls", type=int, default=3)
+    args = ap.parse_args(argv)
+    dev = torch.device("cuda:0")
+    for h, kv, d in ((TARGET["q_heads"], TARGET["kv_heads"], TARGET["head_dim"]),
+                     (DRAFT["q_heads"], DRAFT["kv_heads"], DRAFT["head_dim"])):
+        cache, q = prefill_chunk(h, kv, d, 2048, 8192, device=dev)
+        kp, vp, vs = cache.layer(0)
+        ws = ops.new_workspace(dev, ops.attention_workspace_bytes(1, 1, h, kv, 2048, d, 8192))
+        for _ in range(args.calls):
+            ops.paged_attention(q, kp, vp, vs, cache.block_table(), cache.seq_lens_tensor(), 8192,
+                                q_token_major=True, workspace_tensor=ws)
+        torch.cuda.synchronize()
+        print(f"prefill {h}/{kv}/{d} 2048x8192: {args.calls} calls", flush=True)
+
+
+if __name__ == "__main__":
+    _main()

@@ -77,9 +77,9 @@ def test_prefill_chunk_draft_2048x8192(cuda_device):
                                      (12, 128, 11, 40000), (12, 128, 1000, 1000), (14, 64, 11, 270000)])
 def test_prefill_shapes(cuda_device, h, d, s, t):
     """A first chunk from an empty cache (T = S, triangular mask), odd sizes, short blocks over
-    long contexts and S not a multiple of 16.  A workgroup stages 2048 page ids in LDS at a time:
-    at T = 270,000 (16,875 blocks) every pass-1 key part (of 8) spans two such windows and every
-    pass-2 part (of 2) five, so both passes cross windows with stages in flight."""
+    long contexts and S not a multiple of 16.  A workgroup stages 256 page ids in LDS at a time:
+    at T = 270,000 (16,875 blocks) every pass-1 key part (of 64) spans two such windows and every
+    pass-2 part (of 8) nine, so both passes cross windows with stages in flight."""
     announce(f"prefill {h}/2/{d} S={s} T={t}")
     _prefill_case(cuda_device, h, 2, d, s, t, seed=710 + s + t, chunk_rows=512)
 

@@ -89,6 +89,10 @@ struct AttnArgs {
   int pf_parts;
   // prefill pass 1: key parts per row group (the (max, sum) of each, per row, in stats)
   int pf_split;
+  // prefill pass 2 with parts per row group by its key count (pf_kstar > 0, S a multiple of
+  // the pass's rows per workgroup): at most pf_kstar blocks per part, pf_wh workgroups per
+  // head; pf_parts is then the most parts of any row group (its slots per row group)
+  int pf_kstar, pf_wh;
   // prefill: V dequantized once per call by pass 1 for pass 2.  Per (layer, sequence, KV head)
   // group, vh_stages stages of two page blocks, each D/16 dimension tiles x 64 lanes x 16 bytes
   // in the lane order of the p.V MFMA's A operand (lane (g, n): dimension dt*16 + n, tokens
@@ -1812,6 +1816,16 @@ constexpr int kPrefillMaxParts2 = 8;
 // VGPRs), pass 2 three for head_dim 64 (168) and two for 128 (its 64 fp32 accumulators per lane).
 constexpr int prefill_waves_per_simd(int D, bool OUT) { return !OUT ? 4 : D == 64 ? 3 : 2; }
 
+// Pass 2's parts of row group k (0-based within its head) when they follow its key count:
+// the group's last row sees keys up to T - S + min(S, rows * (k + 1)) - 1, in blocks of 16, cut
+// into parts of at most kstar blocks.  The host plans with T = max_seq_len; the kernel maps
+// its workgroups with the same arguments, so both agree on the grid.
+__host__ __device__ inline int pass2_group_parts(int k, int S, int T, int rows, int kstar) {
+  const int keys = T - S + min(S, rows * (k + 1));
+  const int blocks = keys > 0 ? (keys + kBlock - 1) / kBlock : 0;
+  return max(1, (blocks + kstar - 1) / kstar);
+}
+
 template <int D, bool OUT>
 __global__ __launch_bounds__(64 * prefill_waves(OUT)) __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, OUT))))
 void prefill_kernel(AttnArgs a) {
@@ -1830,9 +1844,22 @@ void prefill_kernel(AttnArgs a) {
   const int grp = zb * a.KV + kvh;
   // the keys of a row group are split in parts, one workgroup each: a.pf_split in pass 1,
   // a.pf_parts in pass 2
-  const int nparts = OUT ? a.pf_parts : a.pf_split;
-  const int split = (int)(blockIdx.x % nparts);
-  const int rgi = (int)(blockIdx.x / nparts);
+  int nparts = OUT ? a.pf_parts : a.pf_split;
+  int split = (int)(blockIdx.x % nparts);
+  int rgi = (int)(blockIdx.x / nparts);
+  if (OUT && a.pf_kstar > 0) {  // parts per row group by its key count: head h, then group k
+    const int rgph = a.S / kPass2Rows;
+    const int h = (int)blockIdx.x / a.pf_wh;
+    int off = (int)blockIdx.x - h * a.pf_wh, k = 0;
+    for (; k < rgph - 1; ++k) {
+      const int pk = pass2_group_parts(k, a.S, a.max_seq_len, kPass2Rows, a.pf_kstar);
+      if (off < pk) break;
+      off -= pk;
+    }
+    nparts = pass2_group_parts(k, a.S, a.max_seq_len, kPass2Rows, a.pf_kstar);
+    split = off;
+    rgi = h * rgph + k;
+  }
   const int row0 = (rgi * W + wave) * ROWS;
 
   // this lane's rows (row tile nt: row row0 + nt*16 + n): q operand and last visible key
@@ -2169,7 +2196,7 @@ void prefill_kernel(AttnArgs a) {
       constexpr int slot_b = kPass2Rows * D * 4;  // bytes per part slot
       // the row group's slots, written and read with 16-byte device-scope (sc1) accesses
       const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-          a.partial + ((int64_t)grp * nrg + rgi) * nparts * (slot_b / 4), (short)0, nparts * slot_b, 0x00020000);
+          a.partial + ((int64_t)grp * nrg + rgi) * a.pf_parts * (slot_b / 4), (short)0, nparts * slot_b, 0x00020000);
       // lane (g, n): row wave*ROWS + nt*16 + n, dimensions dt*16 + 4g .. +3
       const int lofs = ((wave * ROWS + n) * D + 4 * g) * 4;
 #pragma unroll
@@ -2512,6 +2539,7 @@ struct Plan {
   int tpad;                                       // group_kernel: scratch row length (tokens)
   int pf_parts;                                   // prefill pass 2: key parts per row group
   int pf_split;                                   // prefill pass 1: key parts per row group
+  int pf_kstar, pf_wh;                            // prefill pass 2: parts by key count (0: uniform)
   size_t off_vhat;                                // prefill: dequantized V (pass 1 -> pass 2)
   int vh_stages;                                  // prefill: two-block stages per group
   size_t total;                                   // bytes for every layout the call may take
@@ -2555,6 +2583,8 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
   p->tpad = 0;
   p->pf_parts = 1;
   p->pf_split = 1;
+  p->pf_kstar = 0;
+  p->pf_wh = 0;
   p->off_vhat = 0;
   p->vh_stages = 0;
   if (p->n_row_groups > 1) {  // prefill kernels: the per-row (max, sum) of each key part
@@ -2572,6 +2602,33 @@ static bool make_plan(int L, int B, int H, int KV, int S, int D, int max_seq_len
     p->pf_parts = groups * nrg <= (int64_t)(kSyncStatsBytes / 8)
                       ? (int)std::max<int64_t>(1, std::min<int64_t>(std::min(max_parts, kPrefillMaxParts2), pass2_workgroups(D) / (groups * nrg)))
                       : 1;
+    // With S a multiple of the pass's rows, the parts of each row group follow its key count
+    // (the offset-causal mask: the head's later rows see more keys): the fewest blocks per
+    // part that keep the launch within the same budget, so that the workgroups carry nearly
+    // equal work (2048 x 8192, 12/2/128: 504 workgroups of at most 216 blocks instead of 384 of
+    // up to 256, half of the CUs holding one)
+    p->pf_kstar = 0;
+    p->pf_wh = 0;
+    if (p->pf_parts > 1 && S % kPass2Rows == 0) {
+      const int rgph = S / kPass2Rows;
+      const int64_t heads = groups * G;  // (layer, sequence, query head): rgph row groups each
+      for (int kstar = kStageBlocks; kstar < nbk + kStageBlocks; kstar += kStageBlocks) {
+        int wh = 0, pmax = 0;
+        for (int k = 0; k < rgph; ++k) {
+          const int pk = pass2_group_parts(k, S, max_seq_len, kPass2Rows, kstar);
+          wh += pk;
+          pmax = std::max(pmax, pk);
+        }
+        if (heads * wh <= pass2_workgroups(D) && pmax <= kPrefillMaxParts2) {
+          if (pmax > 1) {
+            p->pf_kstar = kstar;
+            p->pf_wh = wh;
+            p->pf_parts = pmax;
+          }
+          break;
+        }
+      }
+    }
     const size_t parts = p->pf_parts > 1
                              ? round_up((size_t)(groups * nrg * p->pf_parts * kPass2Rows * D * 4), 256)
                              : 0;
@@ -2813,7 +2870,7 @@ static bool launch_all(const AttnArgs& a, const Plan& p, int zdim, hipStream_t s
     const dim3 grid((unsigned)((a.R + kPass2Rows - 1) / kPass2Rows), a.KV, zdim);
     constexpr int rows1 = kPass1Tiles * 16 * kPass1Waves;  // pass 1 rows per workgroup
     const dim3 grid1((unsigned)((a.R + rows1 - 1) / rows1) * a.pf_split, grid.y, grid.z),
-        grid2(grid.x * a.pf_parts, grid.y, grid.z);
+        grid2(a.pf_kstar > 0 ? (unsigned)(a.G * a.pf_wh) : grid.x * a.pf_parts, grid.y, grid.z);
     if (phases & SDV_PHASE_QK) hipLaunchKernelGGL((prefill_kernel<D, false>), grid1, dim3(64 * kPass1Waves), 0, st, a);
     if (phases & SDV_PHASE_PV) hipLaunchKernelGGL((prefill_kernel<D, true>), grid2, dim3(64 * kPass2Waves), 0, st, a);
     return true;
@@ -2961,6 +3018,8 @@ static int attention(const void* q, const void* k_pages, const void* v_pages, co
   a.score_stride = p.score_stride;
   a.pf_parts = p.pf_parts;
   a.pf_split = p.pf_split;
+  a.pf_kstar = p.pf_kstar;
+  a.pf_wh = p.pf_wh;
   a.vhat = reinterpret_cast<uint4*>(ws + p.off_vhat);
   a.vh_stages = p.vh_stages;
   // RN(1/sqrt(D)): 1/sqrt(128) = 0.08838834764831845, 1/sqrt(64) = 0.125 exactly

@@ -471,9 +471,10 @@ def prefill_row(torch, dev, h, kv, d, s, t, ref, nrep=2):
         kp, vp, vs = c.layer(0)
         ops.paged_attention(q, kp, vp, vs, bt, sl, t, q_token_major=True, out=out, workspace_tensor=ws)
 
-    # 64 warm-up calls (about 16 ms): the GPU's clocks take that long to ramp after the idle
-    # host work that builds the row's caches (the first 16 calls read about 10% slower)
-    us = time_steps(torch, call, 64, 64, nrep) * 1e3
+    # 200 warm-up calls (about 50 ms): the GPU's clocks take tens of milliseconds of load to
+    # ramp after the idle host work that builds the row's caches (with 4 warm-up calls the
+    # timed calls read about 10% slower, with 64 about 4%)
+    us = time_steps(torch, call, 64, 200, nrep) * 1e3
     keys = s * (t - s) + s * (s + 1) // 2          # visible (row token, key) pairs per head
     flops = 4 * h * keys * d                         # q.k^T and p.V, as the eager path computes them
     executed = 6 * h * keys * d                      # pass 1 recomputes q.k^T

@@ -197,3 +197,30 @@ def test_group_shapes_workspace_and_no_split(lib):
                                               KV, 1, D, T, 0, P, 1 << 40, P, N, mask)
     for mask in (_native.PHASE_QK, _native.PHASE_PV, 4):
         assert phases(mask) == _native.SDV_ERR_UNSUPPORTED
+
+
+def _round256(x):
+    return (x + 255) // 256 * 256
+
+
+def test_prefill_workspace_follows_the_part_plan(lib):
+    """The prefill workspace is the synchronisation prefix, pass 1's (max, sum) per row and key
+    part, pass 2's fp32 part slots (128 rows per row group, as many slots as its most-split row
+    group) and V dequantized once (one 1 KiB tile per 16 dimensions and two blocks).  2048 x 8192
+    (12/2/128): pass 1 in 8 parts (1,536 workgroups of 128 rows), pass 2 by key count, at most 3
+    parts (the last 10 of each head's 16 row groups); with S not a multiple of 128 (S = T =
+    1000) pass 1 takes 7 parts (no fewer than 8 blocks each) and pass 2 splits every row group
+    alike, in 5."""
+    H, KV, D, S, T = 12, 2, 128, 2048, 8192
+    R, groups = H // KV * S, KV
+    want = (_native.SYNC_BYTES + _round256(groups * R * 8 * 8) + _round256(groups * (R // 128) * 3 * 128 * D * 4)
+            + groups * (T // 32) * (D // 16) * 1024)
+    assert lib.sdv_attention_workspace_size(1, 1, H, KV, S, D, T) == want
+    S = T = 1000
+    R = H // KV * S
+    nrg1, nrg2 = -(-R // 128), -(-R // 128)
+    split1 = min(64, (T // 16) // 8, 1536 // (groups * nrg1))
+    parts2 = min(8, (T // 16) // 8, 512 // (groups * nrg2))
+    want = (_native.SYNC_BYTES + _round256(groups * R * 8 * split1) + _round256(groups * nrg2 * parts2 * 128 * D * 4)
+            + groups * (-(-(-(-T // 16)) // 2)) * (D // 16) * 1024)
+    assert lib.sdv_attention_workspace_size(1, 1, H, KV, S, D, T) == want

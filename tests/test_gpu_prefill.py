@@ -84,11 +84,14 @@ def test_prefill_shapes(cuda_device, h, d, s, t):
     _prefill_case(cuda_device, h, 2, d, s, t, seed=710 + s + t, chunk_rows=512)
 
 
-def test_prefill_ragged_batch_token_major(cuda_device):
-    """Two sequences of different lengths in one call, q in the projection layout (B, S, H, D)."""
-    announce("prefill ragged batch, token-major q")
-    g = wl.gen(720, cuda_device)
-    lens, s, h, kv, d = [3000, 700], 96, 12, 2, 128
+@pytest.mark.parametrize("s,h,d", [(96, 12, 128), (256, 12, 128), (256, 14, 64)])
+def test_prefill_ragged_batch_token_major(cuda_device, s, h, d):
+    """Two sequences of different lengths in one call, q in the projection layout (B, S, H, D).
+    With S a multiple of pass 2's 128 rows (S = 256) pass 2's parts follow each row group's key
+    count, planned for the longest sequence: the shorter one's row groups leave parts empty."""
+    announce(f"prefill ragged batch, token-major q, S={s} {h}/2/{d}")
+    g = wl.gen(720 + s + d, cuda_device)
+    lens, kv = [3000, 700], 2
     cache = PagedKVCache(kv, d, batch=2, num_blocks=sum(-(-x // 16) for x in lens) + 5, device=cuda_device,
                          seed=721, growable=False)
     k = torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16)
@@ -122,15 +125,15 @@ def test_prefill_deterministic(cuda_device):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
-@pytest.mark.parametrize("h,d", [(14, 64), (12, 128)])
-def test_prefill_key_parts_repeat_and_replay(cuda_device, h, d):
-    """Pass 2 splits each row group's keys in two parts, and the part that finishes last sums
-    them (a per-row-group counter that it zeroes again): repeated eager calls and the replays
-    of a recorded call -- which reuse one tag -- with eager calls between them are bitwise
-    equal, on a batch of two sequences (two counters per KV head)."""
-    announce(f"prefill {h}/2/{d} key parts: repeats and graph replays")
-    g = wl.gen(740 + d, cuda_device)
-    lens, s, kv = [3000, 1200], 300, 2
+@pytest.mark.parametrize("h,d,s", [(14, 64, 300), (12, 128, 300), (12, 128, 256)])
+def test_prefill_key_parts_repeat_and_replay(cuda_device, h, d, s):
+    """Pass 2 splits each row group's keys in parts, and the part that finishes last sums them
+    (a per-row-group counter that it zeroes again): repeated eager calls and the replays of a
+    recorded call -- which reuse one tag -- with eager calls between them are bitwise equal, on
+    a batch of two sequences (two counters per KV head); S = 256 takes the parts by key count."""
+    announce(f"prefill {h}/2/{d} S={s} key parts: repeats and graph replays")
+    g = wl.gen(740 + d + s, cuda_device)
+    lens, kv = [3000, 1200], 2
     cache = PagedKVCache(kv, d, batch=2, num_blocks=sum(-(-x // 16) for x in lens) + 5, device=cuda_device,
                          seed=741, growable=False)
     cache.prefill(0, torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16),

@@ -1829,8 +1829,8 @@ __host__ __device__ inline int pass2_group_parts(int k, int S, int T, int rows, 
 template <int D, bool OUT>
 __global__ __launch_bounds__(64 * prefill_waves(OUT)) __attribute__((amdgpu_waves_per_eu(prefill_waves_per_simd(D, OUT))))
 void prefill_kernel(AttnArgs a) {
-  // row tiles of 16 rows per wavefront: two in pass 1 (each K operand serves 32 rows), one in
-  // pass 2
+  // row tiles of 16 rows per wavefront (two in both passes: each K operand a wavefront reads
+  // serves 32 rows)
   constexpr int KK = D / 32, DT = D / 16, NT = OUT ? kPass2Tiles : kPass1Tiles, ROWS = NT * 16;
   constexpr int W = prefill_waves(OUT);
   constexpr int DTW = DT / W;  // pass 1: dimension tiles of V each wavefront dequantizes
@@ -1979,11 +1979,12 @@ void prefill_kernel(AttnArgs a) {
   // 1 KiB: block u, 32-dimension slice kk, in the lane order of the MFMA's A operand) and, for
   // pass 2, its dequantized V operand (2 x DT chunks of 1 KiB: pair h of blocks, dimension tile
   // dt, written by pass 1) are the same for every row, so the workgroup loads each chunk once
-  // and shares it through LDS: wavefront w loads chunks w, w + W, ... of stage s + 1 into
-  // registers while the workgroup computes stage s, and writes them to the other LDS buffer
-  // after the next barrier.  One barrier per stage publishes the stage and frees the other
-  // buffer.  Within a stage the q.k^T products of all four blocks go out first, then the
-  // scores, then the p.V products: the MFMA unit has independent work while the VALU rounds.
+  // and shares it through LDS: wavefront w loads chunks w, w + W, ... of stage s + 2 into
+  // registers while the workgroup computes stage s, and writes them to the LDS buffer of stage
+  // s right after the barrier of stage s + 1.  One barrier per stage publishes the stage and
+  // frees the other buffer.  Within a stage the q.k^T products of all four blocks go out
+  // first, then the scores, then the p.V products: the MFMA unit has independent work while
+  // the VALU rounds.
   constexpr int SB = kStageBlocks;
   constexpr int NKC = SB * KK, NC = NKC + (OUT ? (SB / 2) * DT : 0), CPW = NC / W;
   static_assert(CPW * W == NC && NKC % W == 0, "the wavefronts share the chunks evenly");

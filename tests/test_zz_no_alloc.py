@@ -124,8 +124,9 @@ def _batch_cache(dev, layers, kv, d, lens, seed):
 def test_noalloc_group_and_prefill_paths(cuda_device):
     """The per-group kernel (a claim counter that its last workgroup resets) and the head_dim 64
     prefill (a counter per row group that the last key part resets) through the scratch, in the
-    order group -> prefill -> smaller group -> prefill again: every call equals
-    sdv_paged_attention's output bit for bit."""
+    order group -> prefill -> smaller group -> prefill again -> prefill whose pass-2 parts
+    follow each row group's key count: every call equals sdv_paged_attention's output bit for
+    bit."""
     lib = _native.load()
     g = wl.gen(920, cuda_device)
 
@@ -163,6 +164,11 @@ def test_noalloc_group_and_prefill_paths(cuda_device):
 
     announce("noalloc: prefill rows again")
     both(qp, pf, 3000, "prefill again")
+
+    announce("noalloc: prefill rows, 14/2/64, S=256 over T=3000 (pass-2 parts by key count)")
+    qk = torch.randn((1, 14, 256, 64), generator=g, device=cuda_device).to(torch.bfloat16)
+    assert lib.sdv_attention_workspace_size(1, 1, 14, 2, 256, 64, 3000) <= _native.NOALLOC_MAX_WORKSPACE
+    both(qk, pf, 3000, "prefill 256x3000")
 
 
 def test_noalloc_serves_per_layer_launches(cuda_device):

@@ -110,6 +110,33 @@ def test_prefill_ragged_batch_token_major(cuda_device, s, h, d):
         assert_close(out[b:b + 1].transpose(1, 2).cpu(), want, f"ragged b={b} T={t}")
 
 
+def test_prefill_multi_layer_call(cuda_device):
+    """Two layers x two ragged sequences of 128 new rows in one call (q in the projection layout
+    (L, B, S, H, D)): every (layer, sequence) pair has its own pass-1 statistics, dequantized V
+    and pass-2 parts (by key count: S is a multiple of 128), and each output is within the bar
+    of the eager reference."""
+    announce("prefill 2 layers x 2 ragged sequences, S=128, one call")
+    g = wl.gen(725, cuda_device)
+    L, lens, s, h, kv, d = 2, [2500, 900], 128, 12, 2, 128
+    cache = PagedKVCache(kv, d, num_layers=L, batch=2, num_blocks=sum(-(-x // 16) for x in lens) + 5,
+                         device=cuda_device, seed=726, growable=False)
+    slots = None
+    for layer in range(L):
+        k = torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16)
+        v = torch.randn((sum(lens), kv, d), generator=g, device=cuda_device).to(torch.bfloat16)
+        slots = cache.prefill(layer, k, v, lens, slots)
+    q = torch.randn((L, 2, s, h, d), generator=g, device=cuda_device).to(torch.bfloat16)
+    out = ops.paged_attention(q, cache.k_pages, cache.v_pages, cache.v_scales, cache.block_table(),
+                              cache.seq_lens_tensor(), max(lens), q_token_major=True)
+    torch.cuda.synchronize()
+    for layer in range(L):
+        for b, t in enumerate(lens):
+            kc, vc, sc = cache.gather(layer, b)
+            v_hat = oq.dequantize_kv_fp8(vc.cpu()[None], sc.cpu()[None], torch.bfloat16)
+            want = oatt.eager_attention(q[layer, b:b + 1].transpose(1, 2).cpu(), kc.cpu()[None], v_hat)
+            assert_close(out[layer, b:b + 1].transpose(1, 2).cpu(), want, f"layer {layer} b={b} T={t}")
+
+
 def test_prefill_deterministic(cuda_device):
     """Repeated calls are bitwise identical (fixed-order reductions, no atomics)."""
     announce("prefill determinism")
